@@ -1,0 +1,116 @@
+"""ctypes binding of libdispec_hip.so (the C ABI in include/dispec_hip.h).
+
+This is the only place Python touches the native library.  Every entry point takes raw
+device pointers, sizes and a hipStream_t; the helpers here turn torch tensors into those
+arguments and status codes into the exceptions the reference raises for the same misuse
+(ValueError for bad shapes and arguments, RuntimeError for launch failures).
+
+There is no fallback: if the library is missing or fails to load, `lib()` raises, and so
+does every kernel wrapper built on it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libdispec_hip.so"
+
+DSP_BF16, DSP_F16, DSP_F32 = 0, 1, 2
+DSP_OK, DSP_EINVAL, DSP_EALIGN, DSP_EUNSUPPORTED, DSP_EWORKSPACE = 0, -1, -2, -3, -4
+
+# (name, restype, argtypes) for every symbol the header declares.
+_P = c_void_p
+_I64P = POINTER(c_int64)
+SIGNATURES: dict[str, tuple] = {
+    "dsp_error_string": (c_char_p, [c_int]),
+    "dsp_version": (c_int, []),
+    "dsp_kv_append": (c_int, [_P, _P, c_int64, c_int64, _P, _P, c_int64, _P, c_int64, c_int64,
+                              _P, _P]),
+    "dsp_kv_gather_slots": (c_int, [_P, _P, c_int64, c_int64, _P, c_int64, c_int64, _P, _P,
+                                    c_int64, _P, _P]),
+    "dsp_kv_copy_blocks": (c_int, [_P, _P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64,
+                                   c_int64, _P, _P, c_int64, _P, _P]),
+    "dsp_kv_gather": (c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int32, _P, c_int64,
+                              _P, c_int32, c_int64, _P, _P, _P, _P]),
+    "dsp_kv_scatter": (c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int32, _P, c_int64,
+                               _P, c_int32, c_int64, _P, _P, _P, _P]),
+    "dsp_paged_decode_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "dsp_paged_decode_partition_tokens": (c_int, [c_int32, c_int32, c_int32, c_int32]),
+    "dsp_paged_decode": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64,
+                                 _P, c_int64, c_int32, _P, c_int64, _P, c_int32, c_int32,
+                                 c_int32, c_int32, c_float, c_int32, c_int32, _P, c_size_t,
+                                 _P, c_int64, c_int64, c_int32, _P, _P]),
+}
+
+_LIB: ctypes.CDLL | None = None
+
+
+class HipLibraryError(RuntimeError):
+    """libdispec_hip.so is missing or does not export the expected ABI."""
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdispec_hip.so once and bind every symbol of the header."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = Path(os.environ.get("DISPEC_HIP_LIB", LIB_PATH))
+    if not path.exists():
+        raise HipLibraryError(
+            f"{path} is not built; run `python -m dispec_amd.build` (hipcc, gfx950) first")
+    try:
+        handle = ctypes.CDLL(str(path))
+    except OSError as e:  # pragma: no cover - depends on the machine
+        raise HipLibraryError(f"cannot load {path}: {e}") from e
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(handle, name, None)
+        if fn is None:
+            raise HipLibraryError(f"{path} does not export {name}")
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _LIB = handle
+    return handle
+
+
+def error_string(status: int) -> str:
+    return lib().dsp_error_string(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    """Map a C-ABI status to the exception the reference raises for the same misuse."""
+    if status == DSP_OK:
+        return
+    msg = f"{what}: {error_string(status)} (status {status})"
+    if status < 0:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def dtype_code(dtype) -> int:
+    import torch
+    codes = {torch.bfloat16: DSP_BF16, torch.float16: DSP_F16, torch.float32: DSP_F32}
+    if dtype not in codes:
+        raise ValueError(f"unsupported dtype {dtype}")
+    return codes[dtype]
+
+
+def ptr(t) -> int | None:
+    """Device address of a tensor (None for a missing optional tensor)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t) -> int:
+    """hipStream_t of torch's current stream on the tensor's device."""
+    import torch
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_gpu(*tensors) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "dispec_amd kernels run on the GPU only (tensor on "
+                f"{t.device}); there is no CPU path")

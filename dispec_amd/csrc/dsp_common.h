@@ -1,0 +1,99 @@
+// Shared helpers for the gfx950 kernels of libdispec_hip.so (device + host side).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/dispec_hip.h"
+
+#define DSP_HOST_CHECK(cond, code) \
+  do {                             \
+    if (!(cond)) return (code);    \
+  } while (0)
+
+// Launch status: a positive hipError_t, or DSP_OK.
+static inline int dsp_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? DSP_OK : static_cast<int>(e);
+}
+
+static inline bool dsp_aligned(const void* p, int64_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(a)) == 0;
+}
+
+static inline bool dsp_is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+static inline int dsp_log2i(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << r) < x) ++r;
+  return r;
+}
+
+// Largest vector width in {16, 8, 4, 2, 1} bytes dividing every value given.
+static inline int dsp_vec_width(std::initializer_list<int64_t> vals) {
+  int w = 16;
+  for (int64_t v : vals) {
+    while (w > 1 && (v % w) != 0) w >>= 1;
+  }
+  return w;
+}
+
+// ---------------------------------------------------------------- device helpers
+// Byte vectors used for coalesced copies.  16 B per lane is one global_load_dwordx4.
+template <int VEC> struct dsp_vec;
+template <> struct dsp_vec<16> { using type = uint4; };
+template <> struct dsp_vec<8> { using type = uint2; };
+template <> struct dsp_vec<4> { using type = uint32_t; };
+template <> struct dsp_vec<2> { using type = uint16_t; };
+template <> struct dsp_vec<1> { using type = uint8_t; };
+
+// bf16 / fp16 <-> fp32.  bf16 widening is exact (a shift); narrowing rounds to nearest
+// even, as torch's .to(torch.bfloat16) does (NaN kept quiet).
+__device__ __forceinline__ float dsp_bf16lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float dsp_bf16hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+__device__ __forceinline__ uint16_t dsp_f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float dsp_f16lo(uint32_t u) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u & 0xffffu)));
+}
+__device__ __forceinline__ float dsp_f16hi(uint32_t u) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(u >> 16)));
+}
+__device__ __forceinline__ uint16_t dsp_f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));  // round to nearest even
+}
+
+// Cross-lane helpers on one 64-wide wavefront.  DPP row ops act within rows of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float dsp_dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+constexpr int DPP_QUAD_XOR1 = 0xB1;    // quad_perm [1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4E;    // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HMIRROR = 0x141; // lane i <- lane 7-i within each half-row
+constexpr int DPP_ROW_MIRROR = 0x140;  // lane i <- lane 15-i within each row
+
+// Sum over the aligned group of N consecutive lanes (N in 1,2,4,8,16); every lane of
+// the group ends with the group total.
+template <int N>
+__device__ __forceinline__ float dsp_group_sum(float x) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group of 1..16 lanes");
+  if constexpr (N >= 2) x += dsp_dpp<DPP_QUAD_XOR1>(x);
+  if constexpr (N >= 4) x += dsp_dpp<DPP_QUAD_XOR2>(x);
+  if constexpr (N >= 8) x += dsp_dpp<DPP_ROW_HMIRROR>(x);
+  if constexpr (N >= 16) x += dsp_dpp<DPP_ROW_MIRROR>(x);
+  return x;
+}
+
+__device__ __forceinline__ float dsp_shfl_xor(float x, int mask) {
+  int lane = __lane_id();
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
+}
+
+__device__ __forceinline__ float dsp_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -1,0 +1,308 @@
+// Byte-exact KV moves on the paged pool: append (J1), block copy (J2), transport
+// gather (J5a) and scatter (J5c).  All four are HBM-bound copies: every lane moves
+// VEC-byte vectors (16 B = one dwordx4 when strides allow), 64-bit offsets throughout
+// (a full-size pool is far beyond 4 GiB), and each thread issues its loads before its
+// stores so several vectors per lane are in flight.
+#include "dsp_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+// ------------------------------------------------------------------------------- J1
+// One group of `lanes_per_row` lanes per token row; blockIdx.y selects K (0) or V (1).
+// kScatter: dense rows -> pool slots (append); otherwise pool slots -> dense rows.
+template <int VEC, bool kScatter>
+__global__ __launch_bounds__(kThreads) void slot_rows_kernel(
+    char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t num_slots,
+    int64_t pool_stride, const char* __restrict__ k, const char* __restrict__ v,
+    int64_t src_stride, const int64_t* __restrict__ slots, int64_t num_tokens,
+    int32_t chunks_per_row, int32_t lanes_per_row, int32_t rows_per_wg,
+    int32_t* __restrict__ err_count) {
+  using V = typename dsp_vec<VEC>::type;
+  const int64_t row = int64_t(blockIdx.x) * rows_per_wg + threadIdx.x / lanes_per_row;
+  if (row >= num_tokens) return;
+  const int lane = threadIdx.x % lanes_per_row;
+  const int64_t slot = slots[row];
+  if (slot < 0 || slot >= num_slots) {
+    if (lane == 0 && blockIdx.y == 0 && err_count) atomicAdd(err_count, 1);
+    return;
+  }
+  char* dense = const_cast<char*>(blockIdx.y == 0 ? k : v) + row * src_stride;
+  char* pooled = (blockIdx.y == 0 ? k_pool : v_pool) + slot * pool_stride;
+  const char* src = kScatter ? dense : pooled;
+  char* dst = kScatter ? pooled : dense;
+  constexpr int U = 4;
+  for (int c0 = lane; c0 < chunks_per_row; c0 += U * lanes_per_row) {
+    V buf[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * lanes_per_row;
+      if (c < chunks_per_row) buf[u] = reinterpret_cast<const V*>(src)[c];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + u * lanes_per_row;
+      if (c < chunks_per_row) reinterpret_cast<V*>(dst)[c] = buf[u];
+    }
+  }
+}
+
+// Copy `bytes` (a multiple of VEC) from src to dst with the whole workgroup.
+template <int VEC>
+__device__ __forceinline__ void wg_copy(const char* __restrict__ src, char* __restrict__ dst,
+                                        int64_t bytes) {
+  using V = typename dsp_vec<VEC>::type;
+  constexpr int U = 8;
+  const int64_t n = bytes / VEC;
+  const V* s = reinterpret_cast<const V*>(src);
+  V* d = reinterpret_cast<V*>(dst);
+  for (int64_t i0 = threadIdx.x; i0 < n; i0 += int64_t(U) * kThreads) {
+    V buf[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + int64_t(u) * kThreads;
+      if (i < n) buf[u] = s[i];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t i = i0 + int64_t(u) * kThreads;
+      if (i < n) d[i] = buf[u];
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------- J2
+// grid = (num_pairs, num_layers, 2 planes): one whole block of one layer per workgroup.
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void copy_blocks_kernel(
+    const char* __restrict__ src_k, const char* __restrict__ src_v, int64_t src_layer_stride,
+    int64_t src_num_blocks, char* __restrict__ dst_k, char* __restrict__ dst_v,
+    int64_t dst_layer_stride, int64_t dst_num_blocks, int64_t block_bytes,
+    const int32_t* __restrict__ src_blocks, const int32_t* __restrict__ dst_blocks,
+    int32_t* __restrict__ err_count) {
+  const int64_t p = blockIdx.x;
+  const int64_t s = src_blocks[p], d = dst_blocks[p];
+  if (s < 0 || s >= src_num_blocks || d < 0 || d >= dst_num_blocks) {
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && err_count)
+      atomicAdd(err_count, 1);
+    return;
+  }
+  const int64_t l = blockIdx.y;
+  const char* src = (blockIdx.z == 0 ? src_k : src_v) + l * src_layer_stride + s * block_bytes;
+  char* dst = (blockIdx.z == 0 ? dst_k : dst_v) + l * dst_layer_stride + d * block_bytes;
+  wg_copy<VEC>(src, dst, block_bytes);
+}
+
+// --------------------------------------------------------------------------- J5a/J5c
+// grid = (max blocks per sequence, num_layers, 2 * num_seqs).  Block j of sequence b in
+// layer l covers tokens [j*bs, min((j+1)*bs, T_b)): contiguous in the pool (one block)
+// and contiguous in the transport buffer, so it is a single segment copy.
+template <int VEC, bool kGather>
+__global__ __launch_bounds__(kThreads) void transport_kernel(
+    char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t layer_stride,
+    int64_t num_blocks, int64_t row_bytes, int32_t log2_bs,
+    const int32_t* __restrict__ block_tables, int64_t bt_stride,
+    const int64_t* __restrict__ cu_seqlens, int64_t num_layers, char* __restrict__ k_buf,
+    char* __restrict__ v_buf, int32_t* __restrict__ err_count) {
+  const int64_t j = blockIdx.x;
+  const int64_t l = blockIdx.y;
+  const int b = blockIdx.z >> 1;
+  const int plane = blockIdx.z & 1;
+  const int64_t t0 = cu_seqlens[b];
+  const int64_t T = cu_seqlens[b + 1] - t0;
+  const int64_t first = j << log2_bs;
+  if (first >= T) return;
+  const int64_t ntok = min(int64_t(1) << log2_bs, T - first);
+  const int64_t blk = block_tables[int64_t(b) * bt_stride + j];
+  if (blk < 0 || blk >= num_blocks) {
+    if (threadIdx.x == 0 && l == 0 && plane == 0 && err_count) atomicAdd(err_count, 1);
+    return;
+  }
+  char* pool = (plane == 0 ? k_pool : v_pool) + l * layer_stride + (blk << log2_bs) * row_bytes;
+  char* buf = (plane == 0 ? k_buf : v_buf) + (num_layers * t0 + l * T + first) * row_bytes;
+  if constexpr (kGather)
+    wg_copy<VEC>(pool, buf, ntok * row_bytes);
+  else
+    wg_copy<VEC>(buf, pool, ntok * row_bytes);
+}
+
+template <bool kGather>
+int launch_transport(void* k_pool, void* v_pool, int64_t num_layers, int64_t layer_stride,
+                     int64_t num_blocks, int64_t row_bytes, int32_t block_size,
+                     const int32_t* block_tables, int64_t bt_stride, const int64_t* cu_seqlens,
+                     int32_t num_seqs, int64_t max_seqlen, void* k_buf, void* v_buf,
+                     int32_t* err_count, hipStream_t stream) {
+  DSP_HOST_CHECK(k_pool && v_pool && k_buf && v_buf && block_tables && cu_seqlens, DSP_EINVAL);
+  DSP_HOST_CHECK(num_layers > 0 && num_layers <= 65535 && num_blocks > 0 && row_bytes > 0 &&
+                     num_seqs >= 0 && 2 * int64_t(num_seqs) <= 65535 && max_seqlen >= 0,
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(dsp_is_pow2(block_size), DSP_EINVAL);
+  DSP_HOST_CHECK(bt_stride * block_size >= max_seqlen, DSP_EINVAL);
+  DSP_HOST_CHECK(layer_stride >= num_blocks * block_size * row_bytes, DSP_EINVAL);
+  if (num_seqs == 0 || max_seqlen == 0) return DSP_OK;
+  const int vec = dsp_vec_width({row_bytes, layer_stride, int64_t(reinterpret_cast<uintptr_t>(k_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(v_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(k_buf)),
+                                 int64_t(reinterpret_cast<uintptr_t>(v_buf))});
+  const int64_t nblk = (max_seqlen + block_size - 1) / block_size;
+  dim3 grid(static_cast<unsigned>(nblk), static_cast<unsigned>(num_layers), 2u * num_seqs);
+  const int32_t lbs = dsp_log2i(block_size);
+  char* kp = static_cast<char*>(k_pool);
+  char* vp = static_cast<char*>(v_pool);
+  char* kb = static_cast<char*>(k_buf);
+  char* vb = static_cast<char*>(v_buf);
+#define DSP_TRANSPORT(V)                                                                      \
+  transport_kernel<V, kGather><<<grid, kThreads, 0, stream>>>(                                \
+      kp, vp, layer_stride, num_blocks, row_bytes, lbs, block_tables, bt_stride, cu_seqlens, \
+      num_layers, kb, vb, err_count)
+  switch (vec) {
+    case 16: DSP_TRANSPORT(16); break;
+    case 8: DSP_TRANSPORT(8); break;
+    case 4: DSP_TRANSPORT(4); break;
+    case 2: DSP_TRANSPORT(2); break;
+    default: DSP_TRANSPORT(1); break;
+  }
+#undef DSP_TRANSPORT
+  return dsp_launch_status();
+}
+
+}  // namespace
+
+namespace {
+
+template <bool kScatter>
+int launch_slot_rows(void* k_pool, void* v_pool, int64_t num_slots, int64_t pool_stride,
+                     const void* k, const void* v, int64_t dense_stride, const int64_t* slots,
+                     int64_t num_tokens, int64_t row_bytes, int32_t* err_count,
+                     hipStream_t s) {
+  DSP_HOST_CHECK(k_pool && v_pool && k && v && (slots || num_tokens == 0), DSP_EINVAL);
+  DSP_HOST_CHECK(num_slots >= 0 && num_tokens >= 0 && row_bytes > 0, DSP_EINVAL);
+  DSP_HOST_CHECK(pool_stride >= row_bytes && dense_stride >= 0, DSP_EINVAL);
+  if (num_tokens == 0) return DSP_OK;
+  const int vec = dsp_vec_width({row_bytes, pool_stride, dense_stride,
+                                 int64_t(reinterpret_cast<uintptr_t>(k_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(v_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(k)),
+                                 int64_t(reinterpret_cast<uintptr_t>(v))});
+  const int64_t chunks = row_bytes / vec;
+  DSP_HOST_CHECK(chunks < (int64_t(1) << 30), DSP_EINVAL);
+  int lanes = 1;
+  while (lanes < chunks && lanes < kThreads) lanes <<= 1;
+  const int rows_per_wg = kThreads / lanes;
+  const int64_t nwg = (num_tokens + rows_per_wg - 1) / rows_per_wg;
+  DSP_HOST_CHECK(nwg < (int64_t(1) << 31), DSP_EINVAL);
+  dim3 grid(static_cast<unsigned>(nwg), 2u, 1u);
+  char* kp = static_cast<char*>(k_pool);
+  char* vp = static_cast<char*>(v_pool);
+  const char* kd = static_cast<const char*>(k);
+  const char* vd = static_cast<const char*>(v);
+#define DSP_ROWS(V)                                                                          \
+  slot_rows_kernel<V, kScatter><<<grid, kThreads, 0, s>>>(                                   \
+      kp, vp, num_slots, pool_stride, kd, vd, dense_stride, slots, num_tokens,               \
+      static_cast<int32_t>(chunks), lanes, rows_per_wg, err_count)
+  switch (vec) {
+    case 16: DSP_ROWS(16); break;
+    case 8: DSP_ROWS(8); break;
+    case 4: DSP_ROWS(4); break;
+    case 2: DSP_ROWS(2); break;
+    default: DSP_ROWS(1); break;
+  }
+#undef DSP_ROWS
+  return dsp_launch_status();
+}
+
+}  // namespace
+
+extern "C" int dsp_kv_append(void* k_pool, void* v_pool, int64_t num_slots,
+                             int64_t pool_slot_stride_bytes, const void* k, const void* v,
+                             int64_t src_token_stride_bytes, const int64_t* slots,
+                             int64_t num_tokens, int64_t row_bytes, int32_t* err_count,
+                             dsp_stream_t stream) {
+  return launch_slot_rows<true>(k_pool, v_pool, num_slots, pool_slot_stride_bytes, k, v,
+                                src_token_stride_bytes, slots, num_tokens, row_bytes,
+                                err_count, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dsp_kv_gather_slots(const void* k_pool, const void* v_pool, int64_t num_slots,
+                                   int64_t pool_slot_stride_bytes, const int64_t* slots,
+                                   int64_t num_tokens, int64_t row_bytes, void* k_out,
+                                   void* v_out, int64_t out_token_stride_bytes,
+                                   int32_t* err_count, dsp_stream_t stream) {
+  return launch_slot_rows<false>(const_cast<void*>(k_pool), const_cast<void*>(v_pool),
+                                 num_slots, pool_slot_stride_bytes, k_out, v_out,
+                                 out_token_stride_bytes, slots, num_tokens, row_bytes,
+                                 err_count, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dsp_kv_copy_blocks(const void* src_k_pool, const void* src_v_pool,
+                                  int64_t src_layer_stride_bytes, int64_t src_num_blocks,
+                                  void* dst_k_pool, void* dst_v_pool,
+                                  int64_t dst_layer_stride_bytes, int64_t dst_num_blocks,
+                                  int64_t num_layers, int64_t block_bytes,
+                                  const int32_t* src_blocks, const int32_t* dst_blocks,
+                                  int64_t num_pairs, int32_t* err_count, dsp_stream_t stream) {
+  DSP_HOST_CHECK(src_k_pool && src_v_pool && dst_k_pool && dst_v_pool, DSP_EINVAL);
+  DSP_HOST_CHECK((src_blocks && dst_blocks) || num_pairs == 0, DSP_EINVAL);
+  DSP_HOST_CHECK(num_layers > 0 && num_layers <= 65535 && src_num_blocks >= 0 &&
+                     dst_num_blocks >= 0 && block_bytes > 0 && num_pairs >= 0 &&
+                     num_pairs < (int64_t(1) << 31),
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(src_layer_stride_bytes >= src_num_blocks * block_bytes &&
+                     dst_layer_stride_bytes >= dst_num_blocks * block_bytes,
+                 DSP_EINVAL);
+  if (num_pairs == 0) return DSP_OK;
+  const int vec = dsp_vec_width({block_bytes, src_layer_stride_bytes, dst_layer_stride_bytes,
+                                 int64_t(reinterpret_cast<uintptr_t>(src_k_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(src_v_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(dst_k_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(dst_v_pool))});
+  dim3 grid(static_cast<unsigned>(num_pairs), static_cast<unsigned>(num_layers), 2u);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const char* sk = static_cast<const char*>(src_k_pool);
+  const char* sv = static_cast<const char*>(src_v_pool);
+  char* dk = static_cast<char*>(dst_k_pool);
+  char* dv = static_cast<char*>(dst_v_pool);
+#define DSP_COPY(V)                                                                        \
+  copy_blocks_kernel<V><<<grid, kThreads, 0, s>>>(sk, sv, src_layer_stride_bytes,          \
+                                                  src_num_blocks, dk, dv,                  \
+                                                  dst_layer_stride_bytes, dst_num_blocks,  \
+                                                  block_bytes, src_blocks, dst_blocks, err_count)
+  switch (vec) {
+    case 16: DSP_COPY(16); break;
+    case 8: DSP_COPY(8); break;
+    case 4: DSP_COPY(4); break;
+    case 2: DSP_COPY(2); break;
+    default: DSP_COPY(1); break;
+  }
+#undef DSP_COPY
+  return dsp_launch_status();
+}
+
+extern "C" int dsp_kv_gather(const void* k_pool, const void* v_pool, int64_t num_layers,
+                             int64_t pool_layer_stride_bytes, int64_t num_blocks,
+                             int64_t row_bytes, int32_t block_size,
+                             const int32_t* block_tables, int64_t bt_stride,
+                             const int64_t* cu_seqlens, int32_t num_seqs, int64_t max_seqlen,
+                             void* k_buf, void* v_buf, int32_t* err_count,
+                             dsp_stream_t stream) {
+  return launch_transport<true>(const_cast<void*>(k_pool), const_cast<void*>(v_pool),
+                                num_layers, pool_layer_stride_bytes, num_blocks, row_bytes,
+                                block_size, block_tables, bt_stride, cu_seqlens, num_seqs,
+                                max_seqlen, k_buf, v_buf, err_count,
+                                static_cast<hipStream_t>(stream));
+}
+
+extern "C" int dsp_kv_scatter(void* k_pool, void* v_pool, int64_t num_layers,
+                              int64_t pool_layer_stride_bytes, int64_t num_blocks,
+                              int64_t row_bytes, int32_t block_size,
+                              const int32_t* block_tables, int64_t bt_stride,
+                              const int64_t* cu_seqlens, int32_t num_seqs, int64_t max_seqlen,
+                              const void* k_buf, const void* v_buf, int32_t* err_count,
+                              dsp_stream_t stream) {
+  return launch_transport<false>(k_pool, v_pool, num_layers, pool_layer_stride_bytes,
+                                 num_blocks, row_bytes, block_size, block_tables, bt_stride,
+                                 cu_seqlens, num_seqs, max_seqlen, const_cast<void*>(k_buf),
+                                 const_cast<void*>(v_buf), err_count,
+                                 static_cast<hipStream_t>(stream));
+}

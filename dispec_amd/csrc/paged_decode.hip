@@ -1,0 +1,454 @@
+// J3: paged decode attention for gfx950 -- GQA-packed, split-K, online softmax.
+//
+// Semantics follow the reference Triton kernel (dispec/engine/triton_attn.py:59-95):
+// one query token per sequence, query head h reads KV head h / G (:70), fp32
+// accumulation with an online softmax (:86-92), masked tail (:80-85), and the output
+// cast to the cache dtype (:94-95).  The structure is MI355X-specific:
+//
+//  * One workgroup per (partition of `P` tokens, KV head, sequence).  All G query heads
+//    of the KV head are served by the same workgroup, so each K/V row is read from HBM
+//    once rather than G times.
+//  * A row (one token of one KV head, D elements) is loaded by D/8 consecutive lanes,
+//    16 bytes each (global_load_dwordx4), so a wave moves 1 KiB per load instruction.
+//    The slot of every token of the partition is resolved once into LDS first.
+//  * q.k uses v_dot2_f32_{bf16,f16} on packed pairs; the D/8-lane partial sums are
+//    combined with DPP adds inside a 16-lane row (no LDS round trip), which leaves every
+//    lane of the row holding the full scores of the tokens it loaded -- exactly the
+//    weights it needs for its slice of p.V.
+//  * Softmax is tracked in base 2 (log2(e) folded into the scale, v_exp_f32).  Each
+//    row group keeps its own running max; row groups, then waves, are merged with the
+//    usual rescale at the end of the partition.
+//  * Partitions are merged by a second small kernel (log-sum-exp combine) only when a
+//    sequence spans more than one partition.
+#include <float.h>
+
+#include "dsp_common.h"
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kMaxPartition = 1024;
+
+struct Bf16Tag {};
+struct F16Tag {};
+
+template <typename Tag>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc);
+template <>
+__device__ __forceinline__ float dot2<Bf16Tag>(uint32_t a, uint32_t b, float acc) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b),
+                                         acc, false);
+}
+template <>
+__device__ __forceinline__ float dot2<F16Tag>(uint32_t a, uint32_t b, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), acc, false);
+}
+
+template <typename Tag>
+__device__ __forceinline__ void widen2(uint32_t u, float& lo, float& hi) {
+  if constexpr (std::is_same<Tag, Bf16Tag>::value) {
+    lo = dsp_bf16lo(u);
+    hi = dsp_bf16hi(u);
+  } else {
+    lo = dsp_f16lo(u);
+    hi = dsp_f16hi(u);
+  }
+}
+
+template <typename Tag>
+__device__ __forceinline__ uint16_t narrow(float f) {
+  if constexpr (std::is_same<Tag, Bf16Tag>::value)
+    return dsp_f32_to_bf16(f);
+  else
+    return dsp_f32_to_f16(f);
+}
+
+// Geometry of one wave's step over the context for head_dim D.
+template <int D>
+struct Geo {
+  static constexpr int kRowLanes = D / 8;                 // lanes per token row
+  static constexpr int kRowsPerLoad = 64 / kRowLanes;     // rows one load instruction covers
+  static constexpr int kTpl = kRowsPerLoad >= 16 ? 1 : 16 / kRowsPerLoad;  // rows per lane
+  static constexpr int kStep = kRowsPerLoad * kTpl;       // tokens per wave step
+  static constexpr int kWgStep = kStep * kWaves;          // tokens per workgroup step
+};
+
+template <typename Tag, int D, int G, bool kBlockTable>
+__global__ __launch_bounds__(kThreads) void paged_decode_kernel(
+    const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
+    const int32_t* __restrict__ table, int64_t table_stride, int32_t log2_bs,
+    const int32_t* __restrict__ ctx_lens, int32_t max_ctx, float scale_log2, int32_t P,
+    int32_t num_parts, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
+    uint16_t* __restrict__ out, int64_t osb, int64_t osh, int32_t* __restrict__ err_count) {
+  using Gm = Geo<D>;
+  constexpr int RL = Gm::kRowLanes;
+  constexpr int TPL = Gm::kTpl;
+  constexpr int RPL = Gm::kRowsPerLoad;
+  constexpr int Hq_per = G;
+
+  __shared__ int32_t s_slot[kMaxPartition];
+  __shared__ float s_acc[kWaves][G][D];
+  __shared__ float s_m[kWaves][G];
+  __shared__ float s_l[kWaves][G];
+
+  const int part = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const int Hq = gridDim.y * Hq_per;
+  int ctx = ctx_lens[b];
+  if (ctx > max_ctx || ctx < 0) {
+    if (threadIdx.x == 0 && part == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
+    ctx = ctx < 0 ? 0 : max_ctx;
+  }
+  const int nparts = ctx > 0 ? (ctx + P - 1) / P : 1;
+  if (part >= nparts) return;
+  const int start = part * P;
+  const int n = min(P, ctx - start);  // tokens of this partition (<= 0 only when ctx == 0)
+
+  // Resolve the slot of every token of the partition once.
+  for (int i = threadIdx.x; i < P; i += kThreads) {
+    int32_t slot = -1;
+    if (i < n) {
+      const int t = start + i;
+      int64_t s;
+      if constexpr (kBlockTable) {
+        const int64_t blk = table[int64_t(b) * table_stride + (t >> log2_bs)];
+        s = blk * (int64_t(1) << log2_bs) + (t & ((1 << log2_bs) - 1));
+      } else {
+        s = table[int64_t(b) * table_stride + t];
+      }
+      if (s >= 0 && s < num_slots) {
+        slot = static_cast<int32_t>(s);
+      } else if (err_count) {
+        atomicAdd(err_count, 1);
+      }
+    }
+    s_slot[i] = slot;
+  }
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rg = lane / RL;  // row group: which row of a load this lane reads
+  const int c = lane % RL;   // 16-byte chunk of the row: dims [8c, 8c+8)
+
+  uint4 qv[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    qv[g] = *reinterpret_cast<const uint4*>(q + int64_t(b) * qsb + int64_t(kvh * G + g) * qsh + 8 * c);
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) acc[g][d] = 0.f;
+  }
+  __syncthreads();
+
+  const int64_t head_off = int64_t(kvh) * kvs_head + 8 * c;
+  for (int base = wave * Gm::kStep; base < n; base += Gm::kWgStep) {
+    uint4 kr[TPL], vr[TPL];
+    bool valid[TPL];
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      const int slot = s_slot[base + i * RPL + rg];
+      valid[i] = slot >= 0;
+      const int64_t off = int64_t(valid[i] ? slot : 0) * kvs_slot + head_off;
+      if (valid[i]) {
+        kr[i] = *reinterpret_cast<const uint4*>(kc + off);
+        vr[i] = *reinterpret_cast<const uint4*>(vc + off);
+      } else {
+        kr[i] = make_uint4(0, 0, 0, 0);
+        vr[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    float s[TPL][G];
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float p = dot2<Tag>(qv[g].x, kr[i].x, 0.f);
+        p = dot2<Tag>(qv[g].y, kr[i].y, p);
+        p = dot2<Tag>(qv[g].z, kr[i].z, p);
+        p = dot2<Tag>(qv[g].w, kr[i].w, p);
+        p = dsp_group_sum<RL>(p);
+        s[i][g] = valid[i] ? p * scale_log2 : -INFINITY;
+      }
+    }
+    float vf[TPL][8];
+#pragma unroll
+    for (int i = 0; i < TPL; ++i) {
+      widen2<Tag>(vr[i].x, vf[i][0], vf[i][1]);
+      widen2<Tag>(vr[i].y, vf[i][2], vf[i][3]);
+      widen2<Tag>(vr[i].z, vf[i][4], vf[i][5]);
+      widen2<Tag>(vr[i].w, vf[i][6], vf[i][7]);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mx = s[0][g];
+#pragma unroll
+      for (int i = 1; i < TPL; ++i) mx = fmaxf(mx, s[i][g]);
+      const float m_new = fmaxf(m[g], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = dsp_exp2(m[g] - m_use);
+      float lsum = 0.f;
+      float pv[8];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) pv[d] = acc[g][d] * alpha;
+#pragma unroll
+      for (int i = 0; i < TPL; ++i) {
+        const float p = dsp_exp2(s[i][g] - m_use);
+        lsum += p;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) pv[d] = fmaf(p, vf[i][d], pv[d]);
+      }
+      l[g] = l[g] * alpha + lsum;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc[g][d] = pv[d];
+      m[g] = m_new;
+    }
+  }
+
+  // Merge the row groups of this wave (lanes that differ in the bits above log2(RL)).
+#pragma unroll
+  for (int mask = RL; mask < 64; mask <<= 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mo = dsp_shfl_xor(m[g], mask);
+      const float lo = dsp_shfl_xor(l[g], mask);
+      const float M = fmaxf(m[g], mo);
+      const float Mu = M == -INFINITY ? 0.f : M;
+      const float a = dsp_exp2(m[g] - Mu), bb = dsp_exp2(mo - Mu);
+      l[g] = l[g] * a + lo * bb;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const float ao = dsp_shfl_xor(acc[g][d], mask);
+        acc[g][d] = acc[g][d] * a + ao * bb;
+      }
+      m[g] = M;
+    }
+  }
+  if (rg == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int d = 0; d < 8; ++d) s_acc[wave][g][8 * c + d] = acc[g][d];
+      if (c == 0) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  const bool single = nparts == 1;
+  for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    float M = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][g]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float e = dsp_exp2(s_m[w][g] - Mu);
+      L = fmaf(s_l[w][g], e, L);
+      A = fmaf(s_acc[w][g][d], e, A);
+    }
+    const int h = kvh * G + g;
+    if (single) {
+      out[int64_t(b) * osb + int64_t(h) * osh + d] = narrow<Tag>(L > 0.f ? A / L : 0.f);
+    } else {
+      const int64_t row = (int64_t(b) * Hq + h) * num_parts + part;
+      ws_acc[row * D + d] = A;
+      if (d == 0) {
+        ws_ml[2 * row] = M;
+        ws_ml[2 * row + 1] = L;
+      }
+    }
+  }
+}
+
+// Log-sum-exp merge of the partitions of each (sequence, query head).  grid = (Hq, B).
+template <typename Tag>
+__global__ __launch_bounds__(128) void decode_combine_kernel(
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
+    const int32_t* __restrict__ ctx_lens, int32_t max_ctx, int32_t D, int32_t P,
+    int32_t num_parts, uint16_t* __restrict__ out, int64_t osb, int64_t osh) {
+  const int h = blockIdx.x, b = blockIdx.y, Hq = gridDim.x;
+  int ctx = ctx_lens[b];
+  ctx = ctx < 0 ? 0 : (ctx > max_ctx ? max_ctx : ctx);
+  const int nparts = ctx > 0 ? (ctx + P - 1) / P : 1;
+  if (nparts <= 1) return;  // written directly by the partition kernel
+  const int64_t row0 = (int64_t(b) * Hq + h) * num_parts;
+  float M = -INFINITY;
+  for (int p = 0; p < nparts; ++p) M = fmaxf(M, ws_ml[2 * (row0 + p)]);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float L = 0.f;
+  for (int p = 0; p < nparts; ++p)
+    L = fmaf(ws_ml[2 * (row0 + p) + 1], dsp_exp2(ws_ml[2 * (row0 + p)] - Mu), L);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float A = 0.f;
+    for (int p = 0; p < nparts; ++p)
+      A = fmaf(ws_acc[(row0 + p) * D + d], dsp_exp2(ws_ml[2 * (row0 + p)] - Mu), A);
+    out[int64_t(b) * osb + int64_t(h) * osh + d] = narrow<Tag>(A * inv);
+  }
+}
+
+int wg_step_for(int D) {
+  switch (D) {
+    case 16: return Geo<16>::kWgStep;
+    case 32: return Geo<32>::kWgStep;
+    case 64: return Geo<64>::kWgStep;
+    case 128: return Geo<128>::kWgStep;
+    default: return 0;
+  }
+}
+
+template <typename Tag, int D, int G>
+int launch_decode_dg(bool block_mode, dim3 grid, hipStream_t s, const uint16_t* q, int64_t qsb,
+                     int64_t qsh, const uint16_t* kc, const uint16_t* vc, int64_t num_slots,
+                     int64_t kvs_slot, int64_t kvs_head, const int32_t* table,
+                     int64_t table_stride, int32_t log2_bs, const int32_t* ctx_lens,
+                     int32_t max_ctx, float scale_log2, int32_t P, int32_t num_parts,
+                     float* ws_acc, float* ws_ml, uint16_t* out, int64_t osb, int64_t osh,
+                     int32_t* err) {
+  if (block_mode)
+    paged_decode_kernel<Tag, D, G, true><<<grid, kThreads, 0, s>>>(
+        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, table, table_stride, log2_bs,
+        ctx_lens, max_ctx, scale_log2, P, num_parts, ws_acc, ws_ml, out, osb, osh, err);
+  else
+    paged_decode_kernel<Tag, D, G, false><<<grid, kThreads, 0, s>>>(
+        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, table, table_stride, log2_bs,
+        ctx_lens, max_ctx, scale_log2, P, num_parts, ws_acc, ws_ml, out, osb, osh, err);
+  return dsp_launch_status();
+}
+
+template <typename Tag, int D, typename... A>
+int launch_decode_d(int G, A... args) {
+  switch (G) {
+    case 1: return launch_decode_dg<Tag, D, 1>(args...);
+    case 2: return launch_decode_dg<Tag, D, 2>(args...);
+    case 3: return launch_decode_dg<Tag, D, 3>(args...);
+    case 4: return launch_decode_dg<Tag, D, 4>(args...);
+    case 5: return launch_decode_dg<Tag, D, 5>(args...);
+    case 6: return launch_decode_dg<Tag, D, 6>(args...);
+    case 7: return launch_decode_dg<Tag, D, 7>(args...);
+    case 8: return launch_decode_dg<Tag, D, 8>(args...);
+    default: return DSP_EUNSUPPORTED;
+  }
+}
+
+template <typename Tag, typename... A>
+int launch_decode(int D, int G, A... args) {
+  switch (D) {
+    case 16: return launch_decode_d<Tag, 16>(G, args...);
+    case 32: return launch_decode_d<Tag, 32>(G, args...);
+    case 64: return launch_decode_d<Tag, 64>(G, args...);
+    case 128: return launch_decode_d<Tag, 128>(G, args...);
+    default: return DSP_EUNSUPPORTED;
+  }
+}
+
+}  // namespace
+
+extern "C" int dsp_paged_decode_partition_tokens(int32_t B, int32_t KVH, int32_t D,
+                                                 int32_t max_ctx) {
+  const int step = wg_step_for(D);
+  if (step == 0 || B <= 0 || KVH <= 0 || max_ctx <= 0) return step > 0 ? step : 0;
+  // Largest power-of-two multiple of the workgroup step, at most 512, that still gives
+  // the launch enough workgroups to fill 256 CUs several times over.
+  int P = step;
+  while (P * 2 <= 512) P *= 2;
+  while (P > step && int64_t(B) * KVH * ((max_ctx + P - 1) / P) < 2048) P /= 2;
+  return P;
+}
+
+extern "C" size_t dsp_paged_decode_workspace_bytes(int32_t B, int32_t Hq, int32_t D,
+                                                   int32_t max_ctx, int32_t partition_tokens) {
+  if (B <= 0 || Hq <= 0 || D <= 0 || max_ctx <= 0 || partition_tokens <= 0) return 0;
+  const int64_t np = (int64_t(max_ctx) + partition_tokens - 1) / partition_tokens;
+  if (np <= 1) return 0;
+  return size_t(B) * Hq * np * (size_t(D) + 2) * sizeof(float);
+}
+
+extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                const void* k_cache, const void* v_cache, int64_t num_slots,
+                                int64_t kv_stride_slot, int64_t kv_stride_head,
+                                const int32_t* block_table, int64_t bt_stride,
+                                int32_t block_size, const int32_t* slot_table,
+                                int64_t st_stride, const int32_t* ctx_lens, int32_t B,
+                                int32_t Hq, int32_t KVH, int32_t D, float scale,
+                                int32_t max_ctx, int32_t partition_tokens, void* workspace,
+                                size_t workspace_bytes, void* out, int64_t o_stride_b,
+                                int64_t o_stride_h, int32_t dtype, int32_t* err_count,
+                                dsp_stream_t stream) {
+  DSP_HOST_CHECK(q && k_cache && v_cache && ctx_lens && out, DSP_EINVAL);
+  DSP_HOST_CHECK((block_table != nullptr) != (slot_table != nullptr), DSP_EINVAL);
+  DSP_HOST_CHECK(B >= 0 && Hq > 0 && KVH > 0 && Hq % KVH == 0 && max_ctx >= 0 && num_slots >= 0,
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(B <= 65535 && KVH <= 65535 && num_slots < (int64_t(1) << 31), DSP_EINVAL);
+  DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16, DSP_EUNSUPPORTED);
+  const int G = Hq / KVH;
+  const int step = wg_step_for(D);
+  DSP_HOST_CHECK(step > 0 && G >= 1 && G <= 8, DSP_EUNSUPPORTED);
+  if (B == 0) return DSP_OK;
+  // 16-byte vector loads of q and K/V rows.
+  DSP_HOST_CHECK(q_stride_b % 8 == 0 && q_stride_h % 8 == 0 && kv_stride_slot % 8 == 0 &&
+                     kv_stride_head % 8 == 0 && dsp_aligned(q, 16) && dsp_aligned(k_cache, 16) &&
+                     dsp_aligned(v_cache, 16),
+                 DSP_EALIGN);
+  int32_t log2_bs = 0;
+  const int32_t* table = block_table ? block_table : slot_table;
+  int64_t table_stride = block_table ? bt_stride : st_stride;
+  if (block_table) {
+    DSP_HOST_CHECK(dsp_is_pow2(block_size), DSP_EINVAL);
+    log2_bs = dsp_log2i(block_size);
+    DSP_HOST_CHECK(bt_stride * block_size >= max_ctx, DSP_EINVAL);
+  } else {
+    DSP_HOST_CHECK(st_stride >= max_ctx, DSP_EINVAL);
+  }
+  int P = partition_tokens > 0 ? partition_tokens
+                               : dsp_paged_decode_partition_tokens(B, KVH, D, max_ctx);
+  DSP_HOST_CHECK(P % step == 0 && P <= kMaxPartition, DSP_EINVAL);
+  const int num_parts = max_ctx > 0 ? (max_ctx + P - 1) / P : 1;
+  const size_t need = dsp_paged_decode_workspace_bytes(B, Hq, D, max_ctx, P);
+  DSP_HOST_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr), DSP_EWORKSPACE);
+  DSP_HOST_CHECK(need == 0 || dsp_aligned(workspace, 16), DSP_EALIGN);
+  float* ws_acc = static_cast<float*>(workspace);
+  float* ws_ml = need ? ws_acc + int64_t(B) * Hq * num_parts * D : nullptr;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid(static_cast<unsigned>(num_parts), static_cast<unsigned>(KVH), static_cast<unsigned>(B));
+  const uint16_t* qh = static_cast<const uint16_t*>(q);
+  const uint16_t* kh = static_cast<const uint16_t*>(k_cache);
+  const uint16_t* vh = static_cast<const uint16_t*>(v_cache);
+  uint16_t* oh = static_cast<uint16_t*>(out);
+  const bool bm = block_table != nullptr;
+  int st;
+  if (dtype == DSP_BF16)
+    st = launch_decode<Bf16Tag>(D, G, bm, grid, s, qh, q_stride_b, q_stride_h, kh, vh, num_slots,
+                                kv_stride_slot, kv_stride_head, table, table_stride, log2_bs,
+                                ctx_lens, max_ctx, scale_log2, P, num_parts, ws_acc, ws_ml, oh,
+                                o_stride_b, o_stride_h, err_count);
+  else
+    st = launch_decode<F16Tag>(D, G, bm, grid, s, qh, q_stride_b, q_stride_h, kh, vh, num_slots,
+                               kv_stride_slot, kv_stride_head, table, table_stride, log2_bs,
+                               ctx_lens, max_ctx, scale_log2, P, num_parts, ws_acc, ws_ml, oh,
+                               o_stride_b, o_stride_h, err_count);
+  if (st != DSP_OK || num_parts <= 1) return st;
+  dim3 cgrid(static_cast<unsigned>(Hq), static_cast<unsigned>(B));
+  if (dtype == DSP_BF16)
+    decode_combine_kernel<Bf16Tag><<<cgrid, 128, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, D, P,
+                                                         num_parts, oh, o_stride_b, o_stride_h);
+  else
+    decode_combine_kernel<F16Tag><<<cgrid, 128, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, D, P,
+                                                        num_parts, oh, o_stride_b, o_stride_h);
+  return dsp_launch_status();
+}

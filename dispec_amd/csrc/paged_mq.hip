@@ -1,0 +1,309 @@
+// J4: multi-query paged attention (speculative verify, chunked prefill) on MFMA.
+//
+// Semantics: ModelRunner._attention's native branch (dispec/engine/model_runner.py:
+// 160-185) -- for each sequence, SDPA over its paged context with
+// causal_lower_right(q_len, ctx_len) and GQA: query i of a sequence sits at position
+// ctx - q_len + i and sees keys j <= ctx - q_len + i; query head h reads KV head h / G.
+//
+// Layout on gfx950 (64-wide waves, v_mfma_f32_16x16x32_{bf16,f16}):
+//  * A workgroup owns one tile of 16 "packed rows" of one (sequence, KV head); packed
+//    row r is query r / G of query head kvh*G + r % G, so all G heads that share the KV
+//    head ride in the same MFMA tile and every K/V row is loaded once for all of them.
+//  * The 4 waves split the causal key range in 32-key chunks; their softmax states are
+//    merged through LDS at the end.
+//  * Scores are formed transposed, S^T = K . Q^T (keys on M, packed rows on N).  K goes
+//    straight from HBM into the A operand (lane l: key l%16, 8 dims); Q^T is loaded once.
+//    In the 16x16 output layout lane l holds keys 4*(l/16)+j of row l%16, which is
+//    exactly the B operand of O^T = V^T . P^T for a 32-key step -- P never leaves
+//    registers.  Only V needs a transpose: each wave stages its 32-key V chunk in LDS
+//    (row pitch padded by 16 bytes so the transposed 2-byte reads are conflict-free).
+//  * Softmax is online per packed row in base 2; the row max is combined across the 4
+//    lane groups with two cross-lane exchanges.
+#include <float.h>
+
+#include "dsp_common.h"
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct Bf16Tag {};
+struct F16Tag {};
+
+template <typename Tag>
+__device__ __forceinline__ f32x4 mfma32(uint4 a, uint4 b, f32x4 c) {
+  if constexpr (std::is_same<Tag, Bf16Tag>::value)
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+template <typename Tag>
+__device__ __forceinline__ uint16_t narrow(float f) {
+  if constexpr (std::is_same<Tag, Bf16Tag>::value)
+    return dsp_f32_to_bf16(f);
+  else
+    return dsp_f32_to_f16(f);
+}
+
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return uint32_t(lo) | (uint32_t(hi) << 16);
+}
+
+// Slot of context token t of sequence b (block-table addressing), or -1 if out of range.
+__device__ __forceinline__ int64_t mq_slot(const int32_t* __restrict__ bt, int64_t bt_row,
+                                           int32_t log2_bs, int t, int64_t num_slots) {
+  const int64_t blk = bt[bt_row + (t >> log2_bs)];
+  const int64_t s = blk * (int64_t(1) << log2_bs) + (t & ((1 << log2_bs) - 1));
+  return (s >= 0 && s < num_slots) ? s : -1;
+}
+
+template <typename Tag, int D>
+__global__ __launch_bounds__(kThreads) void paged_mq_kernel(
+    const uint16_t* __restrict__ q, int64_t qst, int64_t qsh, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
+    const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
+    int32_t G, float scale_log2, uint16_t* __restrict__ out, int64_t ost, int64_t osh,
+    int32_t* __restrict__ err_count) {
+  constexpr int NKK = D / 32;        // 32-dim K steps of the score MFMA
+  constexpr int NT = D / 16;         // 16-dim output tiles
+  constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
+  constexpr int VPL = 32 * CPR / 64; // V chunks each lane stages per 32-key step
+  constexpr int PITCH = D + 8;       // LDS row pitch of the staged V chunk (elements)
+
+  __shared__ uint16_t s_v[kWaves][32][PITCH];
+  __shared__ float s_m[kWaves][16];
+  __shared__ float s_l[kWaves][16];
+  __shared__ float s_acc[kWaves][16][D + 1];
+
+  const int tile = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int q0 = cu_q[b];
+  const int qlen = cu_q[b + 1] - q0;
+  int ctx = ctx_lens[b];
+  const int rows = qlen * G;
+  const int r0 = tile * 16;
+  if (qlen <= 0 || r0 >= rows) return;
+  const bool bad = ctx > max_ctx || ctx < qlen;
+  if (bad) {
+    if (threadIdx.x == 0 && tile == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
+    ctx = 0;  // no keys: rows are written as zeros
+  }
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = lane & 15;   // packed row within the tile (N index)
+  const int grp = lane >> 4; // lane group: K sub-range of the MFMA operands
+  const int r = r0 + n;
+  const bool row_ok = r < rows && !bad;
+  const int qi = row_ok ? r / G : 0;
+  const int h = kvh * G + (row_ok ? r % G : 0);
+  const int pos_q = ctx - qlen + qi;  // keys 0..pos_q are visible to this row
+  const int r_last = min(r0 + 15, rows - 1);
+  const int kend = bad ? 0 : ctx - qlen + r_last / G + 1;  // keys any row of the tile sees
+  const int64_t bt_row = int64_t(b) * bt_stride;
+  const int64_t head_off = int64_t(kvh) * kvs_head;
+
+  uint4 qop[NKK];
+#pragma unroll
+  for (int kk = 0; kk < NKK; ++kk) {
+    qop[kk] = row_ok ? *reinterpret_cast<const uint4*>(q + int64_t(q0 + qi) * qst + int64_t(h) * qsh +
+                                                       32 * kk + 8 * grp)
+                     : make_uint4(0, 0, 0, 0);
+  }
+
+  float m = -INFINITY, lpart = 0.f;
+  f32x4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int t0 = wave * 32; t0 < kend; t0 += 32 * kWaves) {
+    // K operands of the two 16-key halves: lane holds key t0 + 16*st + n, dims 8*grp+32*kk.
+    uint4 kop[2][NKK];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int key = t0 + 16 * st + n;
+      const int64_t s = key < kend ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk)
+        kop[st][kk] = s >= 0 ? *reinterpret_cast<const uint4*>(kc + s * kvs_slot + head_off +
+                                                                32 * kk + 8 * grp)
+                             : make_uint4(0, 0, 0, 0);
+    }
+    // Stage this step's 32 V rows in the wave's LDS slab (zeros past kend).
+    uint4 vst[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int idx = lane + 64 * i;
+      const int key = t0 + idx / CPR;
+      const int64_t s = key < kend ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
+      vst[i] = s >= 0 ? *reinterpret_cast<const uint4*>(vc + s * kvs_slot + head_off + 8 * (idx % CPR))
+                      : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int idx = lane + 64 * i;
+      *reinterpret_cast<uint4*>(&s_v[wave][idx / CPR][8 * (idx % CPR)]) = vst[i];
+    }
+
+    f32x4 sc[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      sc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk) sc[st] = mfma32<Tag>(kop[st][kk], qop[kk], sc[st]);
+    }
+    // Scale and causal mask; lane holds keys t0 + 16*st + 4*grp + j of packed row n.
+    float s[2][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = t0 + 16 * st + 4 * grp + j;
+        const bool ok = row_ok && key <= pos_q;
+        s[st][j] = ok ? sc[st][j] * scale_log2 : -INFINITY;
+        mx = fmaxf(mx, s[st][j]);
+      }
+    }
+    mx = fmaxf(mx, dsp_shfl_xor(mx, 16));
+    mx = fmaxf(mx, dsp_shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = dsp_exp2(m - m_use);
+    m = m_new;
+    float psum = 0.f;
+    uint16_t pb[8];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float p = dsp_exp2(s[st][j] - m_use);
+        psum += p;
+        pb[4 * st + j] = narrow<Tag>(p);
+      }
+    }
+    lpart = lpart * alpha + psum;
+    const uint4 pop = make_uint4(pack2(pb[0], pb[1]), pack2(pb[2], pb[3]), pack2(pb[4], pb[5]),
+                                 pack2(pb[6], pb[7]));
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] *= alpha;
+
+    // V^T operand: lane needs dim 16*nt + n of keys {4*grp+u} (u<4) and {16+4*grp+u-4}.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const int d = 16 * nt + n;
+      uint16_t v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int kl = u < 4 ? 4 * grp + u : 16 + 4 * grp + (u - 4);
+        v[u] = s_v[wave][kl][d];
+      }
+      const uint4 vop = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]),
+                                   pack2(v[6], v[7]));
+      acc[nt] = mfma32<Tag>(vop, pop, acc[nt]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // Row sums: this lane's keys only so far; add the other three lane groups.
+  lpart += dsp_shfl_xor(lpart, 16);
+  lpart += dsp_shfl_xor(lpart, 32);
+  if (grp == 0) {
+    s_m[wave][n] = m;
+    s_l[wave][n] = lpart;
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_acc[wave][n][16 * nt + 4 * grp + j] = acc[nt][j];
+  __syncthreads();
+
+  for (int idx = threadIdx.x; idx < 16 * D; idx += kThreads) {
+    const int rr = idx / D, d = idx % D;
+    const int row = r0 + rr;
+    if (row >= rows) continue;
+    float M = s_m[0][rr];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][rr]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float e = dsp_exp2(s_m[w][rr] - Mu);
+      L = fmaf(s_l[w][rr], e, L);
+      A = fmaf(s_acc[w][rr][d], e, A);
+    }
+    const int qrow = q0 + row / G, hh = kvh * G + row % G;
+    out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(L > 0.f ? A / L : 0.f);
+  }
+}
+
+template <typename Tag, typename... A>
+int launch_mq(int D, dim3 grid, hipStream_t s, A... args) {
+  switch (D) {
+    case 32: paged_mq_kernel<Tag, 32><<<grid, kThreads, 0, s>>>(args...); break;
+    case 64: paged_mq_kernel<Tag, 64><<<grid, kThreads, 0, s>>>(args...); break;
+    case 128: paged_mq_kernel<Tag, 128><<<grid, kThreads, 0, s>>>(args...); break;
+    default: return DSP_EUNSUPPORTED;
+  }
+  return dsp_launch_status();
+}
+
+}  // namespace
+
+extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                      const void* k_cache, const void* v_cache,
+                                      int64_t num_slots, int64_t kv_stride_slot,
+                                      int64_t kv_stride_head, const int32_t* block_table,
+                                      int64_t bt_stride, int32_t block_size,
+                                      const int32_t* cu_q, const int32_t* ctx_lens, int32_t B,
+                                      int32_t Hq, int32_t KVH, int32_t D, float scale,
+                                      int32_t max_q_len, int32_t max_ctx, void* out,
+                                      int64_t o_stride_t, int64_t o_stride_h, int32_t dtype,
+                                      int32_t* err_count, dsp_stream_t stream) {
+  DSP_HOST_CHECK(q && k_cache && v_cache && block_table && cu_q && ctx_lens && out, DSP_EINVAL);
+  DSP_HOST_CHECK(B >= 0 && B <= 65535 && Hq > 0 && KVH > 0 && KVH <= 65535 && Hq % KVH == 0 &&
+                     max_q_len >= 0 && max_ctx >= 0 && num_slots >= 0,
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16, DSP_EUNSUPPORTED);
+  DSP_HOST_CHECK(D == 32 || D == 64 || D == 128, DSP_EUNSUPPORTED);
+  DSP_HOST_CHECK(dsp_is_pow2(block_size), DSP_EINVAL);
+  DSP_HOST_CHECK(bt_stride * block_size >= max_ctx, DSP_EINVAL);
+  if (B == 0 || max_q_len == 0) return DSP_OK;
+  DSP_HOST_CHECK(q_stride_t % 8 == 0 && q_stride_h % 8 == 0 && kv_stride_slot % 8 == 0 &&
+                     kv_stride_head % 8 == 0 && dsp_aligned(q, 16) && dsp_aligned(k_cache, 16) &&
+                     dsp_aligned(v_cache, 16),
+                 DSP_EALIGN);
+  const int G = Hq / KVH;
+  const int64_t tiles = (int64_t(max_q_len) * G + 15) / 16;
+  DSP_HOST_CHECK(tiles < (int64_t(1) << 31), DSP_EINVAL);
+  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(KVH), static_cast<unsigned>(B));
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* qh = static_cast<const uint16_t*>(q);
+  const uint16_t* kh = static_cast<const uint16_t*>(k_cache);
+  const uint16_t* vh = static_cast<const uint16_t*>(v_cache);
+  uint16_t* oh = static_cast<uint16_t*>(out);
+  const int32_t lbs = dsp_log2i(block_size);
+  if (dtype == DSP_BF16)
+    return launch_mq<Bf16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
+                              kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
+                              ctx_lens, max_ctx, G, scale_log2, oh, o_stride_t, o_stride_h,
+                              err_count);
+  return launch_mq<F16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
+                           kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
+                           ctx_lens, max_ctx, G, scale_log2, oh, o_stride_t, o_stride_h,
+                           err_count);
+}

@@ -1,0 +1,106 @@
+"""Paged attention on the HIP kernels of libdispec_hip.so.
+
+`batched_paged_decode_attention` and `paged_decode_attention` keep the signatures and
+semantics of the reference's Triton wrappers (dispec/engine/triton_attn.py:98-139): the
+same argument meaning, the per-token int32 slot table, `scale = scale or D ** -0.5`, and
+an output allocated like `torch.empty_like(q)`.  They call `dsp_paged_decode`, a
+GQA-packed split-K kernel with a log-sum-exp combine, instead of one Triton program per
+(sequence, query head).
+
+`paged_decode_attention_blocks` is the block-table form (the table is
+[B, max_blocks] int32 instead of [B, max_ctx] slots), the one `ModelRunner` uses.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from dispec_amd import _lib
+
+_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
+            block_table=None, block_size=16, max_ctx=None, partition_tokens=0, out=None,
+            workspace=None):
+    _lib.require_gpu(q, k_cache, v_cache, ctx_lens)
+    if q.dim() != 3 or k_cache.dim() != 3 or v_cache.shape != k_cache.shape:
+        raise ValueError(f"expected q (B, Hq, D) and caches (S, KVH, D); got {tuple(q.shape)}, "
+                         f"{tuple(k_cache.shape)}, {tuple(v_cache.shape)}")
+    B, Hq, D = q.shape
+    S, KVH, Dk = k_cache.shape
+    if Dk != D or Hq != KVH * kv_groups:
+        raise ValueError(f"q has {Hq} heads of {D}, cache {KVH} heads of {Dk}, kv_groups {kv_groups}")
+    if q.dtype not in _DTYPES or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise ValueError(f"q/k/v dtypes {q.dtype}/{k_cache.dtype}/{v_cache.dtype}: "
+                         "the HIP decode kernel takes bf16 or fp16, all the same")
+    if k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
+        raise ValueError("k_cache and v_cache need the same strides with head_dim contiguous")
+    scale = scale or D ** -0.5
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    ctx_lens = ctx_lens.to(torch.int32).contiguous()
+    table = slot_table if slot_table is not None else block_table
+    table = table.to(torch.int32).contiguous()
+    if max_ctx is None:
+        max_ctx = table.shape[1] if slot_table is not None else table.shape[1] * block_size
+    out = torch.empty_like(q) if out is None else out
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
+        raise ValueError("out must have q's shape and dtype with head_dim contiguous")
+    L = _lib.lib()
+    P = partition_tokens or L.dsp_paged_decode_partition_tokens(B, KVH, D, max_ctx)
+    need = L.dsp_paged_decode_workspace_bytes(B, Hq, D, max_ctx, P)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    by_block = slot_table is None
+    _lib.check(L.dsp_paged_decode(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), S,
+        k_cache.stride(0), k_cache.stride(1),
+        table.data_ptr() if by_block else None, table.stride(0) if by_block else 0,
+        block_size, None if by_block else table.data_ptr(),
+        0 if by_block else table.stride(0), ctx_lens.data_ptr(), B, Hq, KVH, D,
+        float(scale), int(max_ctx), int(P), _lib.ptr(workspace), ws_bytes, out.data_ptr(),
+        out.stride(0), out.stride(1), _lib.dtype_code(q.dtype), None, _lib.stream_of(q)),
+        "dsp_paged_decode")
+    return out
+
+
+def batched_paged_decode_attention(q, k_cache, v_cache, slot_table, ctx_lens, kv_groups,
+                                   scale=None):
+    """Paged attention for a batch of single-token queries, one launch (plus combine).
+
+    q:          (B, num_heads, head_dim)
+    k_cache:    (num_slots, num_kv_heads, head_dim), v_cache the same
+    slot_table: (B, max_ctx) int32 slot of each context position (padding ignored)
+    ctx_lens:   (B,) int32 context length of each sequence
+    returns:    (B, num_heads, head_dim) in q's dtype
+    """
+    return _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, slot_table=slot_table)
+
+
+def paged_decode_attention(q, k_cache, v_cache, slots, kv_groups, scale=None):
+    """Paged attention for one query token over `slots` (ctx,) of the cache.
+
+    q: (num_heads, head_dim); returns (num_heads, head_dim).
+    """
+    ctx = slots.shape[0]
+    table = slots.to(torch.int32).reshape(1, ctx)
+    ctx_lens = torch.full((1,), ctx, dtype=torch.int32, device=q.device)
+    return _decode(q.unsqueeze(0), k_cache, v_cache, ctx_lens, kv_groups, scale,
+                   slot_table=table)[0]
+
+
+def paged_decode_attention_blocks(q, k_cache, v_cache, block_table, ctx_lens, kv_groups,
+                                  block_size=16, scale=None, max_ctx=None, partition_tokens=0,
+                                  out=None, workspace=None):
+    """Decode attention addressed by a block table.
+
+    block_table: (B, max_blocks) int32 physical block ids; token j of sequence b lives
+    in slot block_table[b, j // block_size] * block_size + j % block_size.
+    max_ctx: upper bound of ctx_lens (defaults to max_blocks * block_size); it sizes the
+    split-K grid, so a tight bound saves empty workgroups.
+    """
+    return _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, block_table=block_table,
+                   block_size=block_size, max_ctx=max_ctx, partition_tokens=partition_tokens,
+                   out=out, workspace=workspace)

@@ -1,0 +1,166 @@
+/*
+ * dispec_hip.h -- C ABI of the MI355X (gfx950) KV-cache data path.
+ *
+ * One shared library, libdispec_hip.so, exports these entry points. They are the
+ * device side of DiSpec's KV path: append into the paged pool, block copy for
+ * copy-on-write and prefix-cache eviction, paged decode attention (split-K with a
+ * log-sum-exp combine), multi-query paged attention for speculative verify and
+ * chunked prefill, and the transport gather / cross-model map / import scatter.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers (HBM) unless noted.  Strides are in ELEMENTS of
+ *     the named dtype unless the name ends in `_bytes`.
+ *   - The pool layout is the reference's: per layer, K and V are each
+ *     [num_blocks * block_size, num_kv_heads, head_dim]; slot s of a layer is one
+ *     row of num_kv_heads*head_dim contiguous elements (paged_cache.py:3-7, :39).
+ *   - Nothing here allocates device memory or synchronises the host: outputs and the
+ *     split-K workspace are passed in by the caller, and all work is enqueued on
+ *     `stream`.  The library holds no mutable global state.
+ *   - Return value: 0 on success, a negative DSP_E* code for an invalid argument
+ *     (nothing was launched), or a positive hipError_t from the launch.
+ *   - `err_count` (optional, may be NULL) is a device int32 that the kernels
+ *     atomically increment once per out-of-range slot / block id they meet.  Such
+ *     rows are skipped, never read or written out of bounds.
+ */
+#ifndef DISPEC_HIP_H
+#define DISPEC_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t is passed as an opaque pointer so that this header needs no HIP headers. */
+typedef void* dsp_stream_t;
+
+enum dsp_dtype { DSP_BF16 = 0, DSP_F16 = 1, DSP_F32 = 2 };
+
+enum dsp_status {
+  DSP_OK = 0,
+  DSP_EINVAL = -1,        /* null pointer, negative size, inconsistent shape */
+  DSP_EALIGN = -2,        /* a stride or pointer breaks the alignment a kernel needs */
+  DSP_EUNSUPPORTED = -3,  /* dtype / head_dim / group size with no compiled kernel */
+  DSP_EWORKSPACE = -4     /* workspace smaller than dsp_*_workspace_bytes() */
+};
+
+/* Human-readable text for a status code (static storage; never NULL). */
+const char* dsp_error_string(int status);
+
+/* Library version, for the Python loader's sanity check. */
+int dsp_version(void);
+
+/* ------------------------------------------------------------------------------ J1
+ * Slot-mapped append of one layer's new K/V rows into the pool.
+ * Replaces PagedKVCache.write (dispec/kv/paged_cache.py:61-68):
+ *     key[layer].index_copy_(0, slots, k); value[layer].index_copy_(0, slots, v)
+ * and the graph-decoder copy at dispec/engine/cuda_graph.py:70-71.
+ *   k_pool, v_pool : layer base of the pool, num_slots rows of row_bytes at
+ *                    pool_slot_stride_bytes.
+ *   k, v           : num_tokens source rows of row_bytes at src_token_stride_bytes.
+ *   slots          : int64[num_tokens], unique (as index_copy_ requires).
+ * Bit-exact (a byte copy).  K and V go in one launch. */
+int dsp_kv_append(void* k_pool, void* v_pool, int64_t num_slots,
+                  int64_t pool_slot_stride_bytes,
+                  const void* k, const void* v, int64_t src_token_stride_bytes,
+                  const int64_t* slots, int64_t num_tokens, int64_t row_bytes,
+                  int32_t* err_count, dsp_stream_t stream);
+
+/* Slot-list row gather of one layer: k_out[i] = k_pool[slots[i]], same for V.
+ * Replaces PagedKVCache.gather (dispec/kv/paged_cache.py:70-72):
+ *     return key[layer][slots], value[layer][slots]
+ * Out-of-range slots are counted in err_count and their output rows left untouched. */
+int dsp_kv_gather_slots(const void* k_pool, const void* v_pool, int64_t num_slots,
+                        int64_t pool_slot_stride_bytes, const int64_t* slots,
+                        int64_t num_tokens, int64_t row_bytes, void* k_out, void* v_out,
+                        int64_t out_token_stride_bytes, int32_t* err_count,
+                        dsp_stream_t stream);
+
+/* ------------------------------------------------------------------------------ J2
+ * Whole-block copy over every layer, for copy-on-write fork, prefix-cache block copy
+ * and evict-by-copy into a second pool.  The reference shares blocks by refcount only
+ * (dispec/kv/block_manager.py:119-126, dispec/kv/prefix_cache.py:64-70); this is the
+ * data move those metadata operations imply:
+ *     for l, i: dst[l, d_i*bs:(d_i+1)*bs] = src[l, s_i*bs:(s_i+1)*bs]   (K and V)
+ * Source and destination pools may be the same pool.
+ *   block_bytes       : block_size * num_kv_heads * head_dim * elem_size (same in both).
+ *   *_layer_stride_bytes : num_blocks * block_bytes for a contiguous pool.
+ *   src_blocks, dst_blocks : int32[num_pairs] device arrays.  Within one call no block
+ *                    may be both read and written (the copies run concurrently). */
+int dsp_kv_copy_blocks(const void* src_k_pool, const void* src_v_pool,
+                       int64_t src_layer_stride_bytes, int64_t src_num_blocks,
+                       void* dst_k_pool, void* dst_v_pool, int64_t dst_layer_stride_bytes,
+                       int64_t dst_num_blocks, int64_t num_layers, int64_t block_bytes,
+                       const int32_t* src_blocks, const int32_t* dst_blocks,
+                       int64_t num_pairs, int32_t* err_count, dsp_stream_t stream);
+
+/* ------------------------------------------------------------------------ J5a / J5c
+ * Block-table gather of whole sequences over every layer into contiguous transport
+ * buffers, and the inverse scatter.
+ * Replaces PagedKVCache.export_contiguous (paged_cache.py:87-90):
+ *     k_out = key[:, context_slots(block_ids, seq_len)].contiguous()
+ * and PagedKVCache.import_contiguous (paged_cache.py:92-96):
+ *     key[:, context_slots(block_ids, T)] = k
+ * batched over num_seqs sequences.  Sequence b's buffer is the (num_layers, T_b,
+ * num_kv_heads, head_dim) KVPayload layout (dispec/transport/base.py:24-44) and
+ * starts at row num_layers * cu_seqlens[b] of k_buf / v_buf.
+ *   block_tables : int32 [num_seqs, bt_stride] physical block ids.
+ *   cu_seqlens   : int64 [num_seqs + 1] device array of token offsets:
+ *                  T_b = cu_seqlens[b+1] - cu_seqlens[b].
+ *   The pool rows must be contiguous (slot stride == row_bytes), as the reference's
+ *   pool is, so that one block of one layer is a single row_bytes*block_size span.
+ *   max_seqlen   : an upper bound on every T_b (sizes the grid).
+ *   block_size   : tokens per block, a power of two. */
+int dsp_kv_gather(const void* k_pool, const void* v_pool, int64_t num_layers,
+                  int64_t pool_layer_stride_bytes, int64_t num_blocks,
+                  int64_t row_bytes, int32_t block_size,
+                  const int32_t* block_tables, int64_t bt_stride,
+                  const int64_t* cu_seqlens, int32_t num_seqs, int64_t max_seqlen,
+                  void* k_buf, void* v_buf, int32_t* err_count, dsp_stream_t stream);
+
+int dsp_kv_scatter(void* k_pool, void* v_pool, int64_t num_layers,
+                   int64_t pool_layer_stride_bytes, int64_t num_blocks,
+                   int64_t row_bytes, int32_t block_size,
+                   const int32_t* block_tables, int64_t bt_stride,
+                   const int64_t* cu_seqlens, int32_t num_seqs, int64_t max_seqlen,
+                   const void* k_buf, const void* v_buf, int32_t* err_count,
+                   dsp_stream_t stream);
+
+/* ------------------------------------------------------------------------------ J3
+ * Paged decode attention, one query token per sequence, GQA-packed and split-K.
+ * Replaces batched_paged_decode_attention (dispec/engine/triton_attn.py:98-116,
+ * kernel :59-95) and paged_decode_attention (:119-139):
+ *     o[b, h] = softmax_j(scale * q[b, h] . K[slot_j, h / G]) . V[slot_j, h / G]
+ * over the ctx_lens[b] context tokens, accumulated in fp32, written in the cache
+ * dtype.  Keys are addressed either by a per-token slot table (the reference's
+ * signature, slot_table[b, j], block_table == NULL) or by a block table
+ * (block_table[b, j / block_size] * block_size + j % block_size, slot_table == NULL).
+ *   q, out       : [B, Hq, D] with strides (q_stride_b, q_stride_h), D contiguous.
+ *   k/v_cache    : one layer, [num_slots, KVH, D] with strides (kv_stride_slot,
+ *                  kv_stride_head), D contiguous; same strides for K and V.
+ *   ctx_lens     : int32 [B], each in [0, max_ctx].  ctx_len 0 writes zeros.
+ *   partition_tokens : split-K partition length; 0 picks one from the shape.  When a
+ *                  launch needs more than one partition it uses `workspace`
+ *                  (dsp_paged_decode_workspace_bytes) and a second combine kernel.
+ * dtype: DSP_BF16 or DSP_F16.  D in {16, 32, 64, 128}; G = Hq / KVH in 1..8. */
+size_t dsp_paged_decode_workspace_bytes(int32_t B, int32_t Hq, int32_t D, int32_t max_ctx,
+                                        int32_t partition_tokens);
+int dsp_paged_decode_partition_tokens(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx);
+
+int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                     const void* k_cache, const void* v_cache, int64_t num_slots,
+                     int64_t kv_stride_slot, int64_t kv_stride_head,
+                     const int32_t* block_table, int64_t bt_stride, int32_t block_size,
+                     const int32_t* slot_table, int64_t st_stride,
+                     const int32_t* ctx_lens, int32_t B, int32_t Hq, int32_t KVH,
+                     int32_t D, float scale, int32_t max_ctx, int32_t partition_tokens,
+                     void* workspace, size_t workspace_bytes,
+                     void* out, int64_t o_stride_b, int64_t o_stride_h,
+                     int32_t dtype, int32_t* err_count, dsp_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DISPEC_HIP_H */

@@ -1,0 +1,80 @@
+"""The C-ABI library loads and exports every symbol include/dispec_hip.h declares.
+
+CPU only: no kernel is launched.  Host-side argument checks that return before any HIP
+call are exercised through the ABI as well.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared() -> set[str]:
+    text = (ROOT / "include" / "dispec_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:const\s+)?[\w]+\*?\s+\*?(dsp_\w+)\s*\(", text, flags=re.M))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from dispec_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        from dispec_amd.build import build
+        build()
+    return _lib.lib()
+
+
+def test_header_declares_the_expected_entry_points():
+    names = _declared()
+    for n in ("dsp_kv_append", "dsp_kv_copy_blocks", "dsp_kv_gather", "dsp_kv_scatter",
+              "dsp_kv_gather_slots", "dsp_paged_decode", "dsp_paged_decode_workspace_bytes",
+              "dsp_error_string"):
+        assert n in names, n
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from dispec_amd import _lib
+    names = _declared()
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in names if not hasattr(raw, n)]
+    assert not missing, missing
+    assert set(_lib.SIGNATURES) == names, "ctypes prototypes out of sync with the header"
+
+
+def test_status_strings_and_version(lib):
+    from dispec_amd import _lib
+    assert lib.dsp_version() >= 1
+    assert _lib.error_string(0) == "ok"
+    assert "invalid argument" in _lib.error_string(_lib.DSP_EINVAL)
+    assert "no compiled kernel" in _lib.error_string(_lib.DSP_EUNSUPPORTED)
+
+
+def test_host_argument_checks_reject_before_launch(lib):
+    from dispec_amd import _lib
+    # null pools
+    assert lib.dsp_kv_append(None, None, 10, 16, None, None, 16, None, 1, 16, None, None) == \
+        _lib.DSP_EINVAL
+    # empty work is a no-op success even with no device
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.dsp_kv_append(fake, fake, 10, 16, fake, fake, 16, None, 0, 16, None, None) == 0
+    # decode: G = Hq / KVH = 9 has no kernel; a non-power-of-two block size is invalid
+    args = dict(B=1, Hq=18, KVH=2, D=64)
+    st = lib.dsp_paged_decode(fake, 64 * 18, 64, fake, fake, 64, 128, 64, fake, 4, 16, None, 0,
+                              fake, args["B"], args["Hq"], args["KVH"], args["D"], 0.125, 64, 0,
+                              None, 0, fake, 64 * 18, 64, _lib.DSP_BF16, None, None)
+    assert st == _lib.DSP_EUNSUPPORTED
+    st = lib.dsp_paged_decode(fake, 64 * 4, 64, fake, fake, 64, 128, 64, fake, 4, 12, None, 0,
+                              fake, 1, 4, 2, 64, 0.125, 48, 0, None, 0, fake, 256, 64,
+                              _lib.DSP_BF16, None, None)
+    assert st == _lib.DSP_EINVAL
+
+
+def test_partition_and_workspace_sizing(lib):
+    # Qwen3-4B long-context shape: 16 x 32768, KVH 8 -> 512-token partitions
+    assert lib.dsp_paged_decode_partition_tokens(16, 8, 128, 32768) == 512
+    assert lib.dsp_paged_decode_workspace_bytes(16, 32, 128, 32768, 512) == 16 * 32 * 64 * 130 * 4
+    assert lib.dsp_paged_decode_workspace_bytes(4, 14, 64, 500, 512) == 0   # one partition
