@@ -17,7 +17,7 @@ static inline int dsp_launch_status() {
   return e == hipSuccess ? DSP_OK : static_cast<int>(e);
 }
 
-static inline bool dsp_aligned(const void* p, int64_t a) {
+__host__ __device__ static inline bool dsp_aligned(const void* p, int64_t a) {
   return (reinterpret_cast<uintptr_t>(p) % static_cast<uintptr_t>(a)) == 0;
 }
 

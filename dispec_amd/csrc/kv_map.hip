@@ -1,0 +1,292 @@
+// J5b: the cross-model KV map -- an MFMA GEMM whose A operand is the design row
+// gathered from several source layers, with epilogues that round exactly where the
+// reference's bf16 torch ops round, plus the fp32 RoPE strip/apply pass.
+//
+// Reference: CrossModelKVMap.map/_apply and LayerMap.apply (dispec/kv/transfer.py:
+// 243-283, 104-112), strip_rope/apply_rope (:66-80).
+//
+// GEMM: C[M, N] = epilogue(A[M, K] . Bt[N, K]^T), bf16 in, fp32 accumulate.
+//  * A row m, column k lives at a + seg_off[k / seg_len] + m * lda + k % seg_len: the
+//    design row of transfer.py:249 (source layers in map order, each a KVH*D row) is
+//    read straight from the contiguous source buffer, never materialised.
+//  * Bt is the weight stored N x K (K contiguous): W^T for x @ W (transposed once when
+//    the map is loaded), or the F.linear weight itself.
+//  * 128 x 128 output tile per 256-thread workgroup, 64 x 64 per wave as 4 x 4
+//    v_mfma_f32_16x16x32 tiles, K in steps of 32 staged through double-buffered LDS
+//    (row pitch padded to 40 elements: the 16-byte fragment reads are conflict-free).
+//  * Epilogue, per element, in the order the reference rounds:
+//      acc -> [bias mode 1: bf16(bf16(acc) + b)  (x @ W + b, two bf16 ops)]
+//             [bias mode 2: bf16(acc + b)        (F.linear / addmm, one rounding)]
+//             [bias mode 0: bf16(acc)]
+//          -> [act 1: bf16(gelu(y)), exact erf form]
+//          -> [accumulate: bf16(c_old + y)]
+#include <math.h>
+
+#include "dsp_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int PITCH = BK + 8;  // LDS row pitch in bf16 elements
+constexpr int kMaxSegments = 8;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct SegOffsets {
+  int64_t off[kMaxSegments];
+  // Offset of segment i without dynamic indexing (which would put the array in scratch).
+  __device__ __forceinline__ int64_t get(int64_t i) const {
+    int64_t r = off[0];
+#pragma unroll
+    for (int j = 1; j < kMaxSegments; ++j) r = (i == j) ? off[j] : r;
+    return r;
+  }
+};
+
+__device__ __forceinline__ float bf16_round(float x) {
+  return __uint_as_float(uint32_t(dsp_f32_to_bf16(x)) << 16);
+}
+
+// Load the 16-byte chunk (8 elements) of A or Bt at (row, k); zero outside the matrix.
+// kVec: `base` already points at the K tile's segment (the tile never straddles two)
+// and `k` is the column inside it.  Otherwise column k is element k % seg_len of
+// segment k / seg_len and each element is fetched on its own (small, unaligned maps).
+template <bool kVec>
+__device__ __forceinline__ uint4 load_chunk(const uint16_t* __restrict__ base,
+                                            const SegOffsets& seg, int64_t seg_len, int64_t ld,
+                                            int64_t row, int64_t rows, int64_t k, int64_t kabs,
+                                            int64_t K) {
+  if (row >= rows || kabs >= K) return make_uint4(0, 0, 0, 0);
+  if constexpr (kVec) {
+    return *reinterpret_cast<const uint4*>(base + k + row * ld);
+  } else {
+    uint16_t e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t kk = kabs + i;
+      const int64_t s = kk / seg_len;
+      e[i] = kk < K ? base[seg.off[s] + (kk - s * seg_len) + row * ld] : uint16_t(0);
+    }
+    return make_uint4(uint32_t(e[0]) | (uint32_t(e[1]) << 16), uint32_t(e[2]) | (uint32_t(e[3]) << 16),
+                      uint32_t(e[4]) | (uint32_t(e[5]) << 16), uint32_t(e[6]) | (uint32_t(e[7]) << 16));
+  }
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kThreads) void map_gemm_kernel(
+    const uint16_t* __restrict__ a, SegOffsets a_seg, int64_t a_seg_len, int64_t lda,
+    const uint16_t* __restrict__ bt, int64_t ldb, uint16_t* __restrict__ c, int64_t ldc,
+    int64_t M, int64_t N, int64_t K, const uint16_t* __restrict__ bias, int32_t bias_mode,
+    int32_t act, int32_t accumulate) {
+  __shared__ uint16_t sa[2][BM][PITCH];
+  __shared__ uint16_t sb[2][BN][PITCH];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t m0 = int64_t(blockIdx.y) * BM, n0 = int64_t(blockIdx.x) * BN;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+
+  // Each thread stages 2 chunks of A and 2 of Bt per K step: rows tid/4 and tid/4 + 64,
+  // chunk tid % 4 (8 elements) of the 32-wide K slice.
+  const int lr = tid >> 2, lc = (tid & 3) * 8;
+  uint4 ra[2], rb[2];
+  SegOffsets b_seg{};
+  auto fetch = [&](int64_t k0) {
+    // k0 is uniform across the workgroup, so the segment lookup stays scalar.
+    const int64_t s = k0 / a_seg_len;
+    const uint16_t* abase = kVec ? a + a_seg.off[s] : a;
+    const int64_t ak = kVec ? k0 - s * a_seg_len + lc : 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      ra[i] = load_chunk<kVec>(abase, a_seg, a_seg_len, lda, m0 + lr + 64 * i, M, ak, k0 + lc, K);
+      rb[i] = load_chunk<kVec>(bt, b_seg, K, ldb, n0 + lr + 64 * i, N, k0 + lc, k0 + lc, K);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      *reinterpret_cast<uint4*>(&sa[buf][lr + 64 * i][lc]) = ra[i];
+      *reinterpret_cast<uint4*>(&sb[buf][lr + 64 * i][lc]) = rb[i];
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t nk = (K + BK - 1) / BK;
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  const int fr = lane & 15, fk = (lane >> 4) * 8;  // fragment row and k offset
+  for (int64_t kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) fetch((kt + 1) * BK);
+    uint4 fa[4], fb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fa[i] = *reinterpret_cast<const uint4*>(&sa[buf][wm + 16 * i + fr][fk]);
+      fb[i] = *reinterpret_cast<const uint4*>(&sb[buf][wn + 16 * i + fr][fk]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fb[j]),
+                                                            __builtin_bit_cast(bf16x8, fa[i]),
+                                                            acc[i][j], 0, 0, 0);
+    if (kt + 1 < nk) {
+      stash(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // acc[i][j] = C^T tile: lane holds rows n = wn + 16j + 4*(lane/16) + e, column
+  // m = wm + 16i + lane%16 (the MFMA was fed Bt as its A operand).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + wm + 16 * i + fr;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t nb = n0 + wn + 16 * j + 4 * (lane >> 4);
+      uint16_t* dst = c + m * ldc + nb;
+      const bool full = nb + 3 < N && dsp_aligned(dst, 8);
+      uint16_t ybits[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t n = nb + e;
+        if (n >= N) continue;
+        float y = acc[i][j][e];
+        if (bias_mode == 1) {
+          y = bf16_round(bf16_round(y) + dsp_bf16lo(bias[n]));
+        } else if (bias_mode == 2) {
+          y = bf16_round(y + dsp_bf16lo(bias[n]));
+        } else {
+          y = bf16_round(y);
+        }
+        if (act == 1) y = bf16_round(0.5f * y * (1.f + erff(y * 0.70710678118654752f)));
+        if (accumulate) y = bf16_round(dsp_bf16lo(dst[e]) + y);
+        ybits[e] = dsp_f32_to_bf16(y);
+        if (!full) dst[e] = ybits[e];
+      }
+      if (full)
+        *reinterpret_cast<uint2*>(dst) = make_uint2(uint32_t(ybits[0]) | (uint32_t(ybits[1]) << 16),
+                                                    uint32_t(ybits[2]) | (uint32_t(ybits[3]) << 16));
+    }
+  }
+}
+
+// RoPE on (L, T, H, D) rows in fp32: out = x*cos + sign*rot(x)*sin, with
+// rot(x) = cat(-x2, x1) over the two halves of head_dim (transfer.py:61-80: sign -1
+// strips, +1 applies).  Input bf16 or fp32; output fp32, or bf16 rounded to nearest
+// even.  One thread per pair (d, d + D/2) of one head of one token of one layer.
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void rope_kernel(const TI* __restrict__ x, TO* __restrict__ y,
+                                                   int64_t L, int64_t T, int64_t H, int64_t D,
+                                                   int64_t x_layer_stride, int64_t y_layer_stride,
+                                                   const float* __restrict__ cos_t,
+                                                   const float* __restrict__ sin_t, float sign) {
+  const int64_t half = D / 2;
+  const int64_t per_layer = T * H * half;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= L * per_layer) return;
+  const int64_t l = idx / per_layer;
+  int64_t r = idx - l * per_layer;
+  const int64_t t = r / (H * half);
+  r -= t * H * half;
+  const int64_t h = r / half, d = r - h * half;
+  const int64_t xo = l * x_layer_stride + (t * H + h) * D;
+  const int64_t yo = l * y_layer_stride + (t * H + h) * D;
+  auto ld = [](TI v) -> float {
+    if constexpr (sizeof(TI) == 2) return dsp_bf16lo(v); else return v;
+  };
+  auto st = [](float v) -> TO {
+    if constexpr (sizeof(TO) == 2) return dsp_f32_to_bf16(v); else return v;
+  };
+  const float x1 = ld(x[xo + d]), x2 = ld(x[xo + d + half]);
+  const float c1 = cos_t[t * D + d], s1 = sin_t[t * D + d];
+  const float c2 = cos_t[t * D + d + half], s2 = sin_t[t * D + d + half];
+  // x * cos and rot(x) * sin are rounded separately, then added (no fused multiply-add),
+  // the operation order of the reference's elementwise torch ops.
+  const float o1 = __fadd_rn(__fmul_rn(x1, c1), sign * __fmul_rn(-x2, s1));
+  const float o2 = __fadd_rn(__fmul_rn(x2, c2), sign * __fmul_rn(x1, s2));
+  y[yo + d] = st(o1);
+  y[yo + d + half] = st(o2);
+}
+
+}  // namespace
+
+extern "C" int dsp_kv_map_gemm(const void* a, const int64_t* a_segment_offsets,
+                               int32_t num_segments, int64_t segment_len, int64_t lda,
+                               const void* bt, int64_t ldb, void* c, int64_t ldc, int64_t M,
+                               int64_t N, int64_t K, const void* bias, int32_t bias_mode,
+                               int32_t activation, int32_t accumulate, int32_t dtype,
+                               dsp_stream_t stream) {
+  DSP_HOST_CHECK(a && bt && c && a_segment_offsets, DSP_EINVAL);
+  DSP_HOST_CHECK(M >= 0 && N >= 0 && K >= 0 && lda >= 0 && ldb >= K && ldc >= N, DSP_EINVAL);
+  DSP_HOST_CHECK(num_segments >= 1 && num_segments <= kMaxSegments && segment_len > 0 &&
+                     int64_t(num_segments) * segment_len == K,
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(bias_mode >= 0 && bias_mode <= 2 && (bias_mode == 0 || bias) &&
+                     (activation == 0 || activation == 1),
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(dtype == DSP_BF16, DSP_EUNSUPPORTED);
+  if (M == 0 || N == 0) return DSP_OK;
+  SegOffsets seg{};
+  bool vec = dsp_aligned(a, 16) && dsp_aligned(bt, 16) && segment_len % BK == 0 &&
+             lda % 8 == 0 && ldb % 8 == 0;
+  for (int i = 0; i < num_segments; ++i) {
+    seg.off[i] = a_segment_offsets[i];
+    vec = vec && (seg.off[i] % 8 == 0);
+  }
+  const int64_t gm = (M + BM - 1) / BM, gn = (N + BN - 1) / BN;
+  DSP_HOST_CHECK(gm < (int64_t(1) << 31) && gn <= 65535, DSP_EINVAL);
+  dim3 grid(static_cast<unsigned>(gn), static_cast<unsigned>(gm));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const uint16_t* ah = static_cast<const uint16_t*>(a);
+  const uint16_t* bh = static_cast<const uint16_t*>(bt);
+  uint16_t* ch = static_cast<uint16_t*>(c);
+  const uint16_t* biash = static_cast<const uint16_t*>(bias);
+  if (vec)
+    map_gemm_kernel<true><<<grid, kThreads, 0, s>>>(ah, seg, segment_len, lda, bh, ldb, ch, ldc, M,
+                                                    N, K, biash, bias_mode, activation, accumulate);
+  else
+    map_gemm_kernel<false><<<grid, kThreads, 0, s>>>(ah, seg, segment_len, lda, bh, ldb, ch, ldc,
+                                                     M, N, K, biash, bias_mode, activation,
+                                                     accumulate);
+  return dsp_launch_status();
+}
+
+extern "C" int dsp_kv_rope(const void* x, int64_t x_layer_stride, void* y,
+                           int64_t y_layer_stride, int64_t L, int64_t T, int64_t H, int64_t D,
+                           const float* cos_table, const float* sin_table, int32_t direction,
+                           int32_t in_dtype, int32_t out_dtype, dsp_stream_t stream) {
+  DSP_HOST_CHECK(x && y && cos_table && sin_table, DSP_EINVAL);
+  DSP_HOST_CHECK(L >= 0 && T >= 0 && H >= 0 && D > 0 && D % 2 == 0, DSP_EINVAL);
+  DSP_HOST_CHECK(x_layer_stride >= T * H * D && y_layer_stride >= T * H * D, DSP_EINVAL);
+  DSP_HOST_CHECK(direction == 1 || direction == -1, DSP_EINVAL);
+  DSP_HOST_CHECK((in_dtype == DSP_BF16 || in_dtype == DSP_F32) &&
+                     (out_dtype == DSP_BF16 || out_dtype == DSP_F32),
+                 DSP_EUNSUPPORTED);
+  const int64_t n = L * T * H * (D / 2);
+  if (n == 0) return DSP_OK;
+  const int64_t blocks = (n + 255) / 256;
+  DSP_HOST_CHECK(blocks < (int64_t(1) << 31), DSP_EINVAL);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned nb = static_cast<unsigned>(blocks);
+  const float sg = float(direction);
+#define DSP_ROPE(TI, TO)                                                                      \
+  rope_kernel<TI, TO><<<nb, 256, 0, s>>>(static_cast<const TI*>(x), static_cast<TO*>(y), L, T, \
+                                         H, D, x_layer_stride, y_layer_stride, cos_table,    \
+                                         sin_table, sg)
+  if (in_dtype == DSP_BF16 && out_dtype == DSP_BF16) DSP_ROPE(uint16_t, uint16_t);
+  else if (in_dtype == DSP_BF16) DSP_ROPE(uint16_t, float);
+  else if (out_dtype == DSP_BF16) DSP_ROPE(float, uint16_t);
+  else DSP_ROPE(float, float);
+#undef DSP_ROPE
+  return dsp_launch_status();
+}

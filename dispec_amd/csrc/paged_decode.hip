@@ -274,31 +274,60 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   }
 }
 
-// Log-sum-exp merge of the partitions of each (sequence, query head).  grid = (Hq, B).
+// Log-sum-exp merge of the partitions of each (sequence, query head).
+// One wave per (sequence, head), four heads per workgroup: grid = (ceil(Hq/4), B).
+// Lanes first run over partitions (max of m, partition weights 2^(m_p - M), and their
+// l-weighted sum), the weights go through the wave's LDS row, then lanes run over dims
+// and stream the partial accumulators with independent loads.
 template <typename Tag>
-__global__ __launch_bounds__(128) void decode_combine_kernel(
+__global__ __launch_bounds__(256) void decode_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ ctx_lens, int32_t max_ctx, int32_t D, int32_t P,
-    int32_t num_parts, uint16_t* __restrict__ out, int64_t osb, int64_t osh) {
-  const int h = blockIdx.x, b = blockIdx.y, Hq = gridDim.x;
+    int32_t num_parts, int32_t Hq, uint16_t* __restrict__ out, int64_t osb, int64_t osh) {
+  __shared__ float s_w[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = blockIdx.x * 4 + wave, b = blockIdx.y;
+  if (h >= Hq) return;
   int ctx = ctx_lens[b];
   ctx = ctx < 0 ? 0 : (ctx > max_ctx ? max_ctx : ctx);
   const int nparts = ctx > 0 ? (ctx + P - 1) / P : 1;
   if (nparts <= 1) return;  // written directly by the partition kernel
   const int64_t row0 = (int64_t(b) * Hq + h) * num_parts;
   float M = -INFINITY;
-  for (int p = 0; p < nparts; ++p) M = fmaxf(M, ws_ml[2 * (row0 + p)]);
+  for (int p = lane; p < nparts; p += 64) M = fmaxf(M, ws_ml[2 * (row0 + p)]);
+#pragma unroll
+  for (int mask = 1; mask < 64; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
   const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
-  for (int p = 0; p < nparts; ++p)
-    L = fmaf(ws_ml[2 * (row0 + p) + 1], dsp_exp2(ws_ml[2 * (row0 + p)] - Mu), L);
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float A = 0.f;
-    for (int p = 0; p < nparts; ++p)
-      A = fmaf(ws_acc[(row0 + p) * D + d], dsp_exp2(ws_ml[2 * (row0 + p)] - Mu), A);
-    out[int64_t(b) * osb + int64_t(h) * osh + d] = narrow<Tag>(A * inv);
+  float L = 0.f, A0 = 0.f, A1 = 0.f;  // dims lane and lane + 64 (D <= 128)
+  for (int p0 = 0; p0 < nparts; p0 += 64) {
+    const int p = p0 + lane;
+    float w = 0.f;
+    if (p < nparts) {
+      w = dsp_exp2(ws_ml[2 * (row0 + p)] - Mu);
+      L = fmaf(ws_ml[2 * (row0 + p) + 1], w, L);
+    }
+    s_w[wave][lane] = w;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int np = min(64, nparts - p0);
+    const float* src = ws_acc + (row0 + p0) * D;
+#pragma unroll 8
+    for (int k = 0; k < np; ++k) {
+      const float wk = s_w[wave][k];
+      if (lane < D) A0 = fmaf(src[int64_t(k) * D + lane], wk, A0);
+      if (lane + 64 < D) A1 = fmaf(src[int64_t(k) * D + lane + 64], wk, A1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
+#pragma unroll
+  for (int mask = 1; mask < 64; mask <<= 1) L += dsp_shfl_xor(L, mask);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  uint16_t* o = out + int64_t(b) * osb + int64_t(h) * osh;
+  if (lane < D) o[lane] = narrow<Tag>(A0 * inv);
+  if (lane + 64 < D) o[lane + 64] = narrow<Tag>(A1 * inv);
 }
 
 int wg_step_for(int D) {
@@ -443,12 +472,12 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
                                ctx_lens, max_ctx, scale_log2, P, num_parts, ws_acc, ws_ml, oh,
                                o_stride_b, o_stride_h, err_count);
   if (st != DSP_OK || num_parts <= 1) return st;
-  dim3 cgrid(static_cast<unsigned>(Hq), static_cast<unsigned>(B));
+  dim3 cgrid(static_cast<unsigned>((Hq + 3) / 4), static_cast<unsigned>(B));
   if (dtype == DSP_BF16)
-    decode_combine_kernel<Bf16Tag><<<cgrid, 128, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, D, P,
-                                                         num_parts, oh, o_stride_b, o_stride_h);
+    decode_combine_kernel<Bf16Tag><<<cgrid, 256, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, D, P,
+                                                         num_parts, Hq, oh, o_stride_b, o_stride_h);
   else
-    decode_combine_kernel<F16Tag><<<cgrid, 128, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, D, P,
-                                                        num_parts, oh, o_stride_b, o_stride_h);
+    decode_combine_kernel<F16Tag><<<cgrid, 256, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, D, P,
+                                                        num_parts, Hq, oh, o_stride_b, o_stride_h);
   return dsp_launch_status();
 }

@@ -104,3 +104,57 @@ def paged_decode_attention_blocks(q, k_cache, v_cache, block_table, ctx_lens, kv
     return _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, block_table=block_table,
                    block_size=block_size, max_ctx=max_ctx, partition_tokens=partition_tokens,
                    out=out, workspace=workspace)
+
+
+def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_groups,
+                       block_size=16, scale=None, max_q_len=None, max_ctx=None, out=None,
+                       err=None):
+    """Multi-query paged attention: speculative verify, chunked and fresh prefill.
+
+    Per sequence b, rows q[cu_q[b]:cu_q[b+1]] are the last q_len_b tokens of a ctx_b-token
+    context already in the cache, attended with the bottom-right causal mask and GQA
+    (the native path of the reference runner, model_runner.py:160-185).
+
+    q:           (sum q_len, num_heads, head_dim), packed by sequence
+    block_table: (B, max_blocks) int32
+    cu_q:        (B+1,) int32 query offsets;  ctx_lens: (B,) int32 context lengths
+    max_q_len, max_ctx: host-side bounds (computed from cu_q / the table if omitted,
+                 which costs a device->host copy)
+    returns:     (sum q_len, num_heads, head_dim) in q's dtype
+    """
+    _lib.require_gpu(q, k_cache, v_cache, block_table, cu_q, ctx_lens)
+    if q.dim() != 3 or k_cache.dim() != 3 or v_cache.shape != k_cache.shape:
+        raise ValueError(f"expected q (T, Hq, D) and caches (S, KVH, D); got {tuple(q.shape)}, "
+                         f"{tuple(k_cache.shape)}")
+    T, Hq, D = q.shape
+    S, KVH, Dk = k_cache.shape
+    if Dk != D or Hq != KVH * kv_groups:
+        raise ValueError(f"q has {Hq} heads of {D}, cache {KVH} heads of {Dk}, kv_groups {kv_groups}")
+    if q.dtype not in _DTYPES or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise ValueError(f"q/k/v dtypes {q.dtype}/{k_cache.dtype}/{v_cache.dtype}: "
+                         "the HIP kernels take bf16 or fp16, all the same")
+    if k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
+        raise ValueError("k_cache and v_cache need the same strides with head_dim contiguous")
+    scale = scale or D ** -0.5
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    cu_q = cu_q.to(torch.int32).contiguous()
+    ctx_lens = ctx_lens.to(torch.int32).contiguous()
+    block_table = block_table.to(torch.int32).contiguous()
+    B = ctx_lens.numel()
+    if cu_q.numel() != B + 1:
+        raise ValueError(f"cu_q has {cu_q.numel()} entries for {B} sequences")
+    if max_q_len is None:
+        max_q_len = int((cu_q[1:] - cu_q[:-1]).max().item()) if B else 0
+    if max_ctx is None:
+        max_ctx = block_table.shape[1] * block_size
+    out = torch.empty_like(q) if out is None else out
+    if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
+        raise ValueError("out must have q's shape and dtype with head_dim contiguous")
+    _lib.check(_lib.lib().dsp_paged_mq_attention(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), S,
+        k_cache.stride(0), k_cache.stride(1), block_table.data_ptr(), block_table.stride(0),
+        block_size, cu_q.data_ptr(), ctx_lens.data_ptr(), B, Hq, KVH, D, float(scale),
+        int(max_q_len), int(max_ctx), out.data_ptr(), out.stride(0), out.stride(1),
+        _lib.dtype_code(q.dtype), _lib.ptr(err), _lib.stream_of(q)), "dsp_paged_mq_attention")
+    return out

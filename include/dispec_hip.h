@@ -159,6 +159,64 @@ int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                      void* out, int64_t o_stride_b, int64_t o_stride_h,
                      int32_t dtype, int32_t* err_count, dsp_stream_t stream);
 
+/* ------------------------------------------------------------------------------ J4
+ * Multi-query paged attention for speculative verify and chunked prefill.
+ * Replaces the native branch of ModelRunner._attention (dispec/engine/model_runner.py:
+ * 160-185): per sequence b, the last q_len_b = cu_q[b+1] - cu_q[b] context tokens are
+ * queries, and
+ *     out = SDPA(q, K, V, attn_mask=causal_lower_right(q_len_b, ctx_lens[b]),
+ *                enable_gqa=True, scale=scale)
+ * i.e. query i sees keys j <= ctx_lens[b] - q_len_b + i.  The new tokens' K/V must
+ * already be in the cache (the reference writes before attending, :148).
+ *   q, out     : packed [sum q_len, Hq, D], strides (q_stride_t, q_stride_h).
+ *   block_table: int32 [B, bt_stride] (power-of-two block_size).
+ *   cu_q       : int32 [B+1] device offsets; ctx_lens: int32 [B], q_len_b <= ctx <= max_ctx.
+ *   max_q_len  : upper bound of q_len_b (sizes the grid).
+ * dtype DSP_BF16 / DSP_F16; D in {32, 64, 128}; any G = Hq / KVH.  A sequence with
+ * q_len > ctx or ctx > max_ctx is counted in err_count and its rows written as zeros. */
+int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                           const void* k_cache, const void* v_cache, int64_t num_slots,
+                           int64_t kv_stride_slot, int64_t kv_stride_head,
+                           const int32_t* block_table, int64_t bt_stride, int32_t block_size,
+                           const int32_t* cu_q, const int32_t* ctx_lens, int32_t B,
+                           int32_t Hq, int32_t KVH, int32_t D, float scale, int32_t max_q_len,
+                           int32_t max_ctx, void* out, int64_t o_stride_t, int64_t o_stride_h,
+                           int32_t dtype, int32_t* err_count, dsp_stream_t stream);
+
+/* ------------------------------------------------------------------------------ J5b
+ * The cross-model map GEMM: C[M, N] = epilogue(A[M, K] . Bt[N, K]^T), bf16 operands,
+ * fp32 accumulation (MFMA).  Replaces the matmuls of LayerMap.apply
+ * (dispec/kv/transfer.py:104-112) on the design rows of CrossModelKVMap._apply (:249):
+ *   A          : design rows read in place.  Column k of row m is
+ *                a[a_segment_offsets[k / segment_len] + m*lda + k % segment_len]: the
+ *                k-th segment is one source layer's KVH*D row (feature order layer ->
+ *                head -> dim).  a_segment_offsets is a HOST array of num_segments
+ *                (1..8) element offsets; num_segments * segment_len == K.
+ *   Bt         : N x K row-major (K contiguous), leading dimension ldb: W^T for
+ *                x @ W, or an F.linear weight as stored.
+ *   C          : M x N row-major, leading dimension ldc.
+ *   bias_mode  : 0 none, 1 bf16(bf16(acc) + b) (x @ W + b as two bf16 ops),
+ *                2 bf16(acc + b) (F.linear / addmm).  bias is bf16 [N].
+ *   activation : 0 none, 1 gelu (erf form) applied to the rounded value and rounded.
+ *   accumulate : 1 adds the result to the existing C in bf16 (residual add).
+ * dtype: DSP_BF16. */
+int dsp_kv_map_gemm(const void* a, const int64_t* a_segment_offsets, int32_t num_segments,
+                    int64_t segment_len, int64_t lda, const void* bt, int64_t ldb, void* c,
+                    int64_t ldc, int64_t M, int64_t N, int64_t K, const void* bias,
+                    int32_t bias_mode, int32_t activation, int32_t accumulate, int32_t dtype,
+                    dsp_stream_t stream);
+
+/* RoPE strip (direction -1) or apply (+1) on (L, T, H, D) rows in fp32:
+ *     y = x * cos + direction * rotate_half(x) * sin,   rotate_half(x) = cat(-x2, x1)
+ * Replaces strip_rope / apply_rope (dispec/kv/transfer.py:66-80).  cos/sin are fp32
+ * (T, D) tables (rope_tables, :50-58).  x, y: layer strides in elements, rows
+ * contiguous; in_dtype / out_dtype DSP_BF16 or DSP_F32 (bf16 output is rounded to
+ * nearest even, as the reference's store into a bf16 buffer is).  y may alias x. */
+int dsp_kv_rope(const void* x, int64_t x_layer_stride, void* y, int64_t y_layer_stride,
+                int64_t L, int64_t T, int64_t H, int64_t D, const float* cos_table,
+                const float* sin_table, int32_t direction, int32_t in_dtype, int32_t out_dtype,
+                dsp_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -86,3 +86,46 @@ def native_attention(q, k_cache, v_cache, slot_lists, q_lens, scale=None):
 def layer_map(x, weight, bias):
     """LayerMap.apply, dense form (transfer.py:108): x @ W + b in the map dtype."""
     return x @ weight + bias
+
+
+def _rotate_half(x):
+    x1, x2 = x.chunk(2, dim=-1)
+    return torch.cat((-x2, x1), dim=-1)
+
+
+def _apply_rope(x, cos, sin):
+    return x * cos.unsqueeze(1) + _rotate_half(x) * sin.unsqueeze(1)
+
+
+@torch.inference_mode()
+def native_forward(model, token_ids, positions, write_slots, seq_meta, key, value,
+                   block_size: int):
+    """ModelRunner.forward with attn_backend="native" (model_runner.py:127-220), on the
+    CPU: per layer, project, q/k-norm (Qwen3), RoPE, index_copy_ the new K/V into the
+    pool (`key`/`value`: [L, S, KVH, D]), then per sequence SDPA with
+    causal_lower_right over the gathered context.  seq_meta: (block_ids, q_len, ctx_len)
+    tuples.  Returns the normalized hidden states (T, hidden)."""
+    cfg = model.config
+    core = model.model
+    H, KVH = cfg.num_attention_heads, cfg.num_key_value_heads
+    D = getattr(cfg, "head_dim", None) or cfg.hidden_size // H
+    dtype = next(p.dtype for p in model.parameters() if p.is_floating_point())
+    cos, sin = core.rotary_emb(torch.zeros(1, 1, dtype=dtype), positions[None, :])
+    cos, sin = cos[0].to(dtype), sin[0].to(dtype)
+    x = core.embed_tokens(token_ids)
+    T = x.shape[0]
+    for li, layer in enumerate(core.layers):
+        attn = layer.self_attn
+        h = layer.input_layernorm(x)
+        q = attn.q_proj(h).view(T, H, D)
+        k = attn.k_proj(h).view(T, KVH, D)
+        v = attn.v_proj(h).view(T, KVH, D)
+        if hasattr(attn, "q_norm"):
+            q, k = attn.q_norm(q), attn.k_norm(k)
+        q, k = _apply_rope(q, cos, sin), _apply_rope(k, cos, sin)
+        append(key[li], value[li], write_slots, k, v)
+        slot_lists = [context_slots(ids, ctx, block_size) for ids, _, ctx in seq_meta]
+        o = native_attention(q, key[li], value[li], slot_lists, [ql for _, ql, _ in seq_meta])
+        x = x + attn.o_proj(o.reshape(T, H * D))
+        x = x + layer.mlp(layer.post_attention_layernorm(x))
+    return core.norm(x)
