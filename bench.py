@@ -1,20 +1,23 @@
 """Benchmark of the MI355X KV-cache data path (one GPU).
 
-Workload (`value`): config 3 of the benchmark plan -- a Qwen3-4B-shape long-context
-decode step: 36 layers, 32 query heads, 8 KV heads (GQA 4), head_dim 128, block_size 16,
-bf16, batch 16 x 32768-token contexts with random block placement.  One step = for each
-layer, append one token per sequence through the slot mapping (dsp_kv_append) and run
-split-K paged decode attention over the full context (dsp_paged_decode, 512-token
-partitions, LSE combine).  `value` is decode attention microseconds per layer.
+Headline workload (`value`): config 3 of the benchmark plan -- a Qwen3-4B-shape
+long-context decode step: 36 layers, 32 query heads, 8 KV heads (GQA 4), head_dim 128,
+block_size 16, bf16, batch 16 x 32768-token contexts with random block placement.  One
+step = for each layer, append one token per sequence through the slot mapping
+(dsp_kv_append), then split-K paged decode attention over the full context
+(dsp_paged_decode, 512-token partitions, log-sum-exp combine).  `value` is decode
+attention microseconds per layer.
 
-Also reported on the same line:
-  roofline      the decode kernel's achieved HBM GB/s (algorithmic bytes / average launch
-                time from HIP events on the launch stream) against 8 TB/s
+Reported beside it on the same JSON line:
+  roofline      decode's achieved HBM GB/s = algorithmic bytes per launch (K and V of
+                every context token once, plus q, out and the block table) / average
+                launch time from HIP events on the launch stream, against 8 TB/s
   cpu_baseline  the reference's CPU torch path (gather + repeat_interleave + SDPA) on a
                 bounded sample of the same workload, timed on this host
-  aux           GB/s of the byte-moving kernels at bandwidth scale: block-table gather of
-                8 x 4096 tokens of a 28-layer Qwen3-1.7B-layout pool (config 5), the scatter
-                into a 36-layer pool, a prefill-scale append, and copy-on-write block copies
+  aux           the other configurations, each timed kernel-only with device-resident
+                tables: config 2 (decode step), config 4 (copy-on-write fork, suffix
+                append, 5-query verify, evict-by-copy), config 5 (gather, map GEMM,
+                scatter) and a prefill-scale append
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-aux]
 """
@@ -33,6 +36,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
 
 C3 = dict(layers=36, hq=32, kvh=8, d=128, bs=16, batch=16, ctx=32768)
 
@@ -51,6 +55,21 @@ def _fill_randn(torch, t, seed: int) -> None:
         t[i].normal_(generator=g)
 
 
+def _time_gpu(torch, fn, iters: int, warmup: int = 2) -> float:
+    """Average seconds per call of fn, HIP events on torch's current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    a, b = _events(torch)
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters / 1e3
+
+
+# ------------------------------------------------------------------------------ config 3
 def bench_decode(torch, steps: int, warmup: int) -> dict:
     from dispec_amd import _lib
     from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
@@ -61,8 +80,7 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
     dev = "cuda"
     nb_seq = ctx // bs
     NB = B * nb_seq
-    _log(f"allocating a {L}-layer pool of {NB} blocks "
-         f"({2 * L * NB * bs * KVH * D * 2 / 1e9:.1f} GB)")
+    _log(f"config 3: {L}-layer pool of {NB} blocks ({2 * L * NB * bs * KVH * D * 2 / 1e9:.1f} GB)")
     cache = PagedKVCache(L, NB, bs, KVH, D, dtype=torch.bfloat16, device=dev)
     _fill_randn(torch, cache.key, 3001)
     _fill_randn(torch, cache.value, 3002)
@@ -93,7 +111,7 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
             if ev is not None:
                 ev[layer][1].record()
 
-    _log(f"decode: warmup {warmup} steps, partition {P} tokens")
+    _log(f"config 3: warmup {warmup} steps, partition {P} tokens")
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -101,26 +119,22 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
     ev = [list(_events(torch)) for _ in range(L)]
     decode_ms = []
     t0, t1 = _events(torch)
+    torch.cuda.synchronize()
     t0.record()
-    for i in range(steps):
+    for _ in range(steps):
         step(ev)
         torch.cuda.synchronize()
         decode_ms.extend(e[0].elapsed_time(e[1]) for e in ev)
     t1.record()
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
-    _log(f"decode: {steps} steps in {total_ms:.1f} ms")
-    kv_bytes = B * ctx * KVH * D * 2 * 2
-    alg_bytes = kv_bytes + 2 * B * Hq * D * 2 + B * nb_seq * 4
+    _log(f"config 3: {steps} steps in {total_ms:.1f} ms")
+    alg_bytes = B * ctx * KVH * D * 2 * 2 + 2 * B * Hq * D * 2 + B * nb_seq * 4
     avg_s = statistics.mean(decode_ms) / 1e3
-    achieved = alg_bytes / avg_s / 1e9
-    # parity spot-check of one layer at full size: shape and finiteness here, the
-    # exact checks live in tests/
     assert torch.isfinite(out).all()
-    res = dict(
-        us_per_layer=avg_s * 1e6, median_us_per_layer=statistics.median(decode_ms) * 1e3,
-        ms_per_step=total_ms / steps, alg_bytes=alg_bytes, achieved_gbps=achieved,
-        partition_tokens=P)
+    res = dict(us_per_layer=avg_s * 1e6, median_us_per_layer=statistics.median(decode_ms) * 1e3,
+               ms_per_step=total_ms / steps, alg_bytes=alg_bytes,
+               achieved_gbps=alg_bytes / avg_s / 1e9, partition_tokens=P)
     del cache, q, k_new, v_new, out, ws
     torch.cuda.empty_cache()
     return res
@@ -135,8 +149,7 @@ def bench_cpu_baseline(torch) -> dict:
     c = C3
     Hq, KVH, D, bs, ctx = c["hq"], c["kvh"], c["d"], c["bs"], c["ctx"]
     nseq, B = 2, c["batch"]
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
     nb = nseq * ctx // bs
     g = torch.Generator().manual_seed(3101)
     kc = torch.randn((nb * bs, KVH, D), generator=g).to(torch.bfloat16)
@@ -151,9 +164,9 @@ def bench_cpu_baseline(torch) -> dict:
         ref_torch.decode_repeat_kv_sdpa(q, kc, vc, slot_lists, Hq // KVH)
         times.append(time.perf_counter() - t)
     per_layer = statistics.median(times[1:]) * (B / nseq)
-    return dict(value=per_layer * 1e6, unit="us/layer", cores=torch.get_num_threads(),
-                kind="port",
-                sample=f"1 layer, {nseq} of {B} sequences x {ctx} tokens, median of "
+    return dict(value=round(per_layer * 1e6, 1), unit="us/layer",
+                cores=torch.get_num_threads(), kind="port",
+                sample=f"config 3, 1 layer, {nseq} of {B} sequences x {ctx} tokens, median of "
                        f"{len(times) - 1} after 1 warmup, scaled x{B // nseq}",
                 cpu_model=_cpu_model())
 
@@ -169,71 +182,218 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def _time_gpu(torch, fn, iters: int, warmup: int = 2) -> float:
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    a, b = _events(torch)
-    a.record()
-    for _ in range(iters):
-        fn()
-    b.record()
-    torch.cuda.synchronize()
-    return a.elapsed_time(b) / iters / 1e3
-
-
-def bench_aux(torch) -> dict:
-    """GB/s of gather / scatter / append / block copy at bandwidth scale."""
+# ------------------------------------------------------------------------------ config 2
+def bench_c2(torch) -> dict:
+    """Qwen2.5-1.5B decode step: 28 layers, Hq 12, KVH 2, D 128, B 64, ctx ~U[512, 4096],
+    blocks scattered over a pool of 1.25x the tokens; per layer append + decode."""
+    from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
     from dispec_amd.kv.paged_cache import PagedKVCache
 
-    res = {}
+    L, Hq, KVH, D, bs, B = 28, 12, 2, 128, 16, 64
     dev = "cuda"
-    # config 5: Qwen3-1.7B-layout source pool, 8 requests x 4096 tokens, random blocks
+    gcpu = torch.Generator().manual_seed(2001)
+    ctx = torch.randint(512, 4097, (B,), generator=gcpu)
+    need = [-(-int(n) // bs) for n in ctx]
+    NB = int(sum(need) * 1.25)
+    cache = PagedKVCache(L, NB, bs, KVH, D, device=dev)
+    _fill_randn(torch, cache.key, 2002)
+    _fill_randn(torch, cache.value, 2003)
+    perm = torch.randperm(NB, generator=gcpu).tolist()
+    tables, at = [], 0
+    for n in need:
+        tables.append(perm[at:at + n])
+        at += n
+    bt = cache.block_table(tables)
+    ctx_lens = ctx.to(torch.int32).to(dev)
+    g = torch.Generator(device=dev).manual_seed(2004)
+    q = torch.randn((L, B, Hq, D), generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn((L, B, KVH, D), generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn((L, B, KVH, D), generator=g, device=dev).to(torch.bfloat16)
+    wslots = torch.tensor([t[(int(n) - 1) // bs] * bs + (int(n) - 1) % bs
+                           for t, n in zip(tables, ctx)], device=dev)
+    out = torch.empty((L, B, Hq, D), dtype=torch.bfloat16, device=dev)
+    max_ctx = int(ctx.max())
+
+    def step():
+        for layer in range(L):
+            cache.write(layer, wslots, kn[layer], vn[layer])
+            paged_decode_attention_blocks(q[layer], cache.key[layer], cache.value[layer], bt,
+                                          ctx_lens, Hq // KVH, block_size=bs, max_ctx=max_ctx,
+                                          out=out[layer])
+
+    def decode_only():
+        for layer in range(L):
+            paged_decode_attention_blocks(q[layer], cache.key[layer], cache.value[layer], bt,
+                                          ctx_lens, Hq // KVH, block_size=bs, max_ctx=max_ctx,
+                                          out=out[layer])
+
+    step_s = _time_gpu(torch, step, 5)
+    dec_s = _time_gpu(torch, decode_only, 5) / L
+    cache.check_errors()
+    kv_bytes = int(ctx.sum()) * KVH * D * 2 * 2
+    res = {"c2_step_us_per_layer": step_s / L * 1e6, "c2_decode_us_per_layer": dec_s * 1e6,
+           "c2_decode_GBps": kv_bytes / dec_s / 1e9}
+    del cache
+    torch.cuda.empty_cache()
+    return res
+
+
+# ------------------------------------------------------------------------------ config 4
+def bench_c4(torch) -> dict:
+    """Qwen3-1.7B shape (28 L, Hq 16, KVH 8, D 128): 32 sequences share a 2050-token
+    prefix, fork it copy-on-write (the partial block is copied per sequence), append
+    suffixes ~U[64, 512], run a 5-query causal verify over the paged cache, then evict 10%
+    of the live blocks by copying them into a spill pool."""
+    from dispec_amd.engine.hip_attn import paged_mq_attention
+    from dispec_amd.kv.paged_cache import PagedKVCache
+
+    L, Hq, KVH, D, bs, S, prefix, K = 28, 16, 8, 128, 16, 32, 2050, 5
+    dev = "cuda"
+    gcpu = torch.Generator().manual_seed(4001)
+    suffix = torch.randint(64, 513, (S,), generator=gcpu).tolist()
+    NB = 1536
+    cache = PagedKVCache(L, NB, bs, KVH, D, device=dev)
+    mgr = cache.manager
+    owner = 1000
+    mgr.allocate(owner, prefix)
+    g = torch.Generator(device=dev).manual_seed(4002)
+    pk = torch.randn((prefix, KVH, D), generator=g, device=dev).to(torch.bfloat16)
+    pslots = cache.context_slots(mgr.block_table(owner).block_ids, prefix)
+    for layer in range(L):
+        cache.write(layer, pslots, pk, pk)
+    # copy-on-write fork of the partial last block for every sequence
+    pairs = []
+    for s in range(S):
+        _, p = mgr.cow_fork(owner, s)
+        pairs += p
+    src = torch.tensor([p[0] for p in pairs], dtype=torch.int32, device=dev)
+    dst = torch.tensor([p[1] for p in pairs], dtype=torch.int32, device=dev)
+    cow_s = _time_gpu(torch, lambda: cache.copy_blocks_device(cache, src, dst), 20)
+    cow_bytes = 2 * 2 * L * len(pairs) * cache.block_bytes
+    # suffix + draft tokens: one append per layer for all 32 sequences
+    rows, wslots = [], []
+    for s in range(S):
+        for _ in range(suffix[s] + K):
+            blk, off = mgr.append_token(s)
+            wslots.append(blk * bs + off)
+        rows.append(suffix[s] + K)
+    wslots_t = torch.tensor(wslots, device=dev)
+    n = len(wslots)
+    kr = torch.randn((n, KVH, D), generator=g, device=dev).to(torch.bfloat16)
+    app_s = _time_gpu(torch, lambda: cache.write(3, wslots_t, kr, kr), 20)
+    # 5-query verify over ctx = prefix + suffix + 5
+    ctx = [prefix + suffix[s] + K for s in range(S)]
+    bt = cache.block_table([mgr.block_table(s).block_ids for s in range(S)])
+    cu = torch.arange(0, (S + 1) * K, K, dtype=torch.int32, device=dev)
+    ctx_t = torch.tensor(ctx, dtype=torch.int32, device=dev)
+    q = torch.randn((L, S * K, Hq, D), generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty((L, S * K, Hq, D), dtype=torch.bfloat16, device=dev)
+    max_ctx = bt.shape[1] * bs
+
+    def verify():
+        for layer in range(L):
+            paged_mq_attention(q[layer], cache.key[layer], cache.value[layer], bt, cu, ctx_t,
+                               Hq // KVH, block_size=bs, max_q_len=K, max_ctx=max_ctx,
+                               out=out[layer])
+
+    ver_s = _time_gpu(torch, verify, 10) / L
+    shared = (prefix // bs) * bs          # full prefix blocks, read by every sequence
+    unique_tokens = shared + sum(c - shared for c in ctx)
+    logical_tokens = sum(ctx)
+    flops = 4 * sum(ctx) * K * Hq * D
+    # evict 10% of live blocks by copying them into a spill pool
+    live = sorted({b for s in range(S) for b in mgr.block_table(s).block_ids}
+                  | set(mgr.block_table(owner).block_ids))
+    nev = max(1, len(live) // 10)
+    spill = PagedKVCache(L, nev, bs, KVH, D, device=dev)
+    esrc = torch.tensor(live[:nev], dtype=torch.int32, device=dev)
+    edst = torch.arange(nev, dtype=torch.int32, device=dev)
+    ev_s = _time_gpu(torch, lambda: spill.copy_blocks_device(cache, esrc, edst), 20)
+    cache.check_errors()
+    spill.check_errors()
+    res = {
+        "c4_cow_pairs": len(pairs), "c4_cow_us": cow_s * 1e6, "c4_cow_GBps": cow_bytes / cow_s / 1e9,
+        "c4_append_rows": n, "c4_append_GBps": 2 * 2 * n * cache.row_bytes / app_s / 1e9,
+        "c4_verify_us_per_layer": ver_s * 1e6,
+        "c4_verify_unique_GBps": unique_tokens * KVH * D * 4 / ver_s / 1e9,
+        "c4_verify_logical_GBps": logical_tokens * KVH * D * 4 / ver_s / 1e9,
+        "c4_verify_TFLOPs": flops / ver_s / 1e12,
+        "c4_evict_blocks": nev, "c4_evict_us": ev_s * 1e6,
+        "c4_evict_GBps": 2 * 2 * L * nev * cache.block_bytes / ev_s / 1e9,
+    }
+    del cache, spill
+    torch.cuda.empty_cache()
+    return res
+
+
+# ------------------------------------------------------------------------------ config 5
+def bench_c5(torch) -> dict:
+    """Gather Qwen3-1.7B paged KV (28 L) of 8 requests x 4096 tokens into contiguous
+    buffers, map each of 36 target layers from source layer round(i*27/35) with a bf16
+    1024x1024 map (weights ~N(0, 1/1024)) for K and V, scatter into a randomly placed
+    Qwen3-4B-layout pool (36 L)."""
+    from dispec_amd.kv.paged_cache import PagedKVCache
+    from dispec_amd.kv.transfer import LayerMap
+
     Ls, Lt, KVH, D, bs, R, T = 28, 36, 8, 128, 16, 8, 4096
+    dev = "cuda"
     nb = R * T // bs
     NB = int(nb * 1.25)
     src = PagedKVCache(Ls, NB, bs, KVH, D, device=dev)
-    _fill_randn(torch, src.key, 3201)
-    _fill_randn(torch, src.value, 3202)
-    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(3203))[:nb].view(R, T // bs)
-    seqs = [(perm[i].tolist(), T) for i in range(R)]
-    sec = _time_gpu(torch, lambda: src.export_batch(seqs), 10)
-    moved = 2 * 2 * Ls * R * T * src.row_bytes        # read + write, K and V
-    res["gather_c5_GBps"] = moved / sec / 1e9
-    res["gather_c5_us"] = sec * 1e6
+    _fill_randn(torch, src.key, 5001)
+    _fill_randn(torch, src.value, 5002)
+    gcpu = torch.Generator().manual_seed(5003)
+    perm = torch.randperm(NB, generator=gcpu)[:nb].view(R, T // bs)
+    bt = perm.to(torch.int32).to(dev)
+    cu = torch.arange(0, (R + 1) * T, T, dtype=torch.int64, device=dev)
+    kbuf = torch.empty((Ls * R * T, KVH, D), dtype=torch.bfloat16, device=dev)
+    vbuf = torch.empty_like(kbuf)
+    g_s = _time_gpu(torch, lambda: src.gather_into(bt, cu, T, kbuf, vbuf), 10)
     src.check_errors()
-    kbuf, vbuf, cu = src.export_batch(seqs)
-    del src, kbuf, vbuf
+    moved = 2 * 2 * Ls * R * T * src.row_bytes
+    del src
     torch.cuda.empty_cache()
-    # scatter of a 36-layer mapped buffer into a randomly placed Qwen3-4B-layout pool
+    # the map: per request b its payload is (Ls, T, KVH, D) at rows Ls*T*b; map over all
+    # 8 x 4096 tokens at once by treating the buffer as (R, Ls, T, kv) and the design row
+    # of target layer i as source layer round(i*27/35) of every request
+    kv = KVH * D
+    g = torch.Generator(device=dev).manual_seed(5004)
+    maps = []
+    for i in range(Lt):
+        w = torch.randn((kv, kv), generator=g, device=dev) / 32
+        maps.append(LayerMap((int(round(i * 27 / 35)),), torch.zeros(kv, device=dev),
+                             weight=w).to(dev, torch.bfloat16))
+    mk = torch.empty((Lt * R * T, KVH, D), dtype=torch.bfloat16, device=dev)
+    mv = torch.empty_like(mk)
+
+    def run_map():
+        # one launch per (target layer, K|V): the 8 requests are the GEMM's batch
+        for buf, outb in ((kbuf, mk), (vbuf, mv)):
+            ob = outb.view(R, Lt, T, kv)
+            for i, m in enumerate(maps):
+                m.apply_into(buf, [m.source_layers[0] * T * kv], kv, kv, T, ob[:, i],
+                             batch=R, a_batch_stride=Ls * T * kv, c_batch_stride=Lt * T * kv)
+
+    m_s = _time_gpu(torch, run_map, 3, warmup=1)
+    flops = 2 * 2 * Lt * R * T * kv * kv
+    # scatter into a 36-layer target pool
     tgt = PagedKVCache(Lt, NB, bs, KVH, D, device=dev)
-    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(3204))[:nb].view(R, T // bs)
-    tables = [perm[i].tolist() for i in range(R)]
-    kb = torch.randn((Lt * R * T, KVH, D), device=dev).to(torch.bfloat16)
-    vb = torch.randn((Lt * R * T, KVH, D), device=dev).to(torch.bfloat16)
-    cu = [i * T for i in range(R + 1)]
-    sec = _time_gpu(torch, lambda: tgt.import_batch(tables, kb, vb, cu), 10)
-    res["scatter_c5_GBps"] = 2 * 2 * Lt * R * T * tgt.row_bytes / sec / 1e9
-    res["scatter_c5_us"] = sec * 1e6
+    perm = torch.randperm(NB, generator=gcpu)[:nb].view(R, T // bs)
+    bt2 = perm.to(torch.int32).to(dev)
+    s_s = _time_gpu(torch, lambda: tgt.scatter_from(bt2, cu, T, mk, mv), 10)
     tgt.check_errors()
-    del kb, vb
-    # prefill-scale append: 32768 token rows (2 KiB each) into random slots of one layer
+    # prefill-scale append of 32768 rows (2 KiB) into random slots of one layer
     n = 32768
-    slots = torch.randperm(tgt.num_slots, generator=torch.Generator().manual_seed(3205))[:n].to(dev)
-    kr = torch.randn((n, KVH, D), device=dev).to(torch.bfloat16)
-    vr = torch.randn((n, KVH, D), device=dev).to(torch.bfloat16)
-    sec = _time_gpu(torch, lambda: tgt.write(3, slots, kr, vr), 20)
-    res["append_prefill_GBps"] = 2 * 2 * n * tgt.row_bytes / sec / 1e9
-    # decode-step append (16 rows): latency
-    sec = _time_gpu(torch, lambda: tgt.write(3, slots[:16], kr[:16], vr[:16]), 50)
-    res["append_decode16_us"] = sec * 1e6
-    # copy-on-write / evict block copies: 1024 block pairs over 36 layers
-    pairs_perm = torch.randperm(NB, generator=torch.Generator().manual_seed(3206))
-    src_ids, dst_ids = pairs_perm[:1024].tolist(), pairs_perm[1024:2048].tolist()
-    sec = _time_gpu(torch, lambda: tgt.copy_blocks_from(tgt, src_ids, dst_ids), 10)
-    res["copy_blocks_GBps"] = 2 * 2 * Lt * 1024 * tgt.block_bytes / sec / 1e9
-    tgt.check_errors()
-    del tgt
+    slots = torch.randperm(tgt.num_slots, generator=gcpu)[:n].to(dev)
+    kr, vr = mk[:n], mv[:n]
+    a_s = _time_gpu(torch, lambda: tgt.write(3, slots, kr, vr), 20)
+    res = {"c5_gather_us": g_s * 1e6, "c5_gather_GBps": moved / g_s / 1e9,
+           "c5_map_ms": m_s * 1e3, "c5_map_TFLOPs": flops / m_s / 1e12,
+           "c5_map_mfma_frac": flops / m_s / 1e12 / PEAK_BF16_TFLOPS,
+           "c5_scatter_us": s_s * 1e6,
+           "c5_scatter_GBps": 2 * 2 * Lt * R * T * tgt.row_bytes / s_s / 1e9,
+           "append_prefill_GBps": 2 * 2 * n * tgt.row_bytes / a_s / 1e9}
+    del tgt, kbuf, vbuf, mk, mv
     torch.cuda.empty_cache()
     return res
 
@@ -248,8 +408,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the KV data path has no cross-GPU exchange in "
-              "this build (sharding is by sequence or KV head, see the design notes); run "
-              "with --gpus 1", file=sys.stderr)
+              "this build (it would shard by sequence or KV head); run with --gpus 1",
+              file=sys.stderr)
         return 2
     import torch
     if not torch.cuda.is_available():
@@ -257,7 +417,11 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     dec = bench_decode(torch, args.steps, args.warmup)
-    aux = {} if args.no_aux else bench_aux(torch)
+    aux = {}
+    if not args.no_aux:
+        for name, fn in (("config 2", bench_c2), ("config 4", bench_c4), ("config 5", bench_c5)):
+            _log(f"{name}")
+            aux.update(fn(torch))
     cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)
     line = {
         "metric": "paged decode attn us/layer (Qwen3-4B shape, 16 x 32768 ctx)",
@@ -280,10 +444,11 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbps"], 1),
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(dec["achieved_gbps"] / PEAK_HBM_GBPS, 4),
-                     "traffic": None, "kernel": "paged_decode_kernel + decode_combine_kernel",
+                     "traffic": None,
+                     "kernel": "paged_decode_kernel + decode_combine_kernel",
                      "alg_bytes_per_launch": dec["alg_bytes"]},
         "decode_GBps": round(dec["achieved_gbps"], 1),
-        "aux": {k: round(v, 2) for k, v in aux.items()},
+        "aux": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in aux.items()},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -48,8 +48,8 @@ SIGNATURES: dict[str, tuple] = {
                                        c_int32, c_float, c_int32, c_int32, _P, c_int64, c_int64,
                                        c_int32, _P, _P]),
     "dsp_kv_map_gemm": (c_int, [_P, _I64P, c_int32, c_int64, c_int64, _P, c_int64, _P, c_int64,
-                                c_int64, c_int64, c_int64, _P, c_int32, c_int32, c_int32, c_int32,
-                                _P]),
+                                c_int64, c_int64, c_int64, c_int32, c_int64, c_int64, _P, c_int32,
+                                c_int32, c_int32, c_int32, _P]),
     "dsp_kv_rope": (c_int, [_P, c_int64, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P,
                             c_int32, c_int32, c_int32, _P]),
 }

@@ -79,8 +79,10 @@ __global__ __launch_bounds__(kThreads) void map_gemm_kernel(
     const uint16_t* __restrict__ a, SegOffsets a_seg, int64_t a_seg_len, int64_t lda,
     const uint16_t* __restrict__ bt, int64_t ldb, uint16_t* __restrict__ c, int64_t ldc,
     int64_t M, int64_t N, int64_t K, const uint16_t* __restrict__ bias, int32_t bias_mode,
-    int32_t act, int32_t accumulate) {
+    int32_t act, int32_t accumulate, int64_t a_batch_stride, int64_t c_batch_stride) {
   __shared__ uint16_t sa[2][BM][PITCH];
+  a += int64_t(blockIdx.z) * a_batch_stride;
+  c += int64_t(blockIdx.z) * c_batch_stride;
   __shared__ uint16_t sb[2][BN][PITCH];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -190,6 +192,7 @@ __global__ __launch_bounds__(256) void rope_kernel(const TI* __restrict__ x, TO*
                                                    int64_t x_layer_stride, int64_t y_layer_stride,
                                                    const float* __restrict__ cos_t,
                                                    const float* __restrict__ sin_t, float sign) {
+#pragma clang fp contract(off)
   const int64_t half = D / 2;
   const int64_t per_layer = T * H * half;
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -210,10 +213,11 @@ __global__ __launch_bounds__(256) void rope_kernel(const TI* __restrict__ x, TO*
   const float x1 = ld(x[xo + d]), x2 = ld(x[xo + d + half]);
   const float c1 = cos_t[t * D + d], s1 = sin_t[t * D + d];
   const float c2 = cos_t[t * D + d + half], s2 = sin_t[t * D + d + half];
-  // x * cos and rot(x) * sin are rounded separately, then added (no fused multiply-add),
-  // the operation order of the reference's elementwise torch ops.
-  const float o1 = __fadd_rn(__fmul_rn(x1, c1), sign * __fmul_rn(-x2, s1));
-  const float o2 = __fadd_rn(__fmul_rn(x2, c2), sign * __fmul_rn(x1, s2));
+  // x * cos and rot(x) * sin are rounded separately, then added (contraction into a fused
+  // multiply-add is off for this kernel): the operation order of the reference's
+  // elementwise torch ops.
+  const float o1 = x1 * c1 + sign * (-x2 * s1);
+  const float o2 = x2 * c2 + sign * (x1 * s2);
   y[yo + d] = st(o1);
   y[yo + d + half] = st(o2);
 }
@@ -223,7 +227,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const TI* __restrict__ x, TO*
 extern "C" int dsp_kv_map_gemm(const void* a, const int64_t* a_segment_offsets,
                                int32_t num_segments, int64_t segment_len, int64_t lda,
                                const void* bt, int64_t ldb, void* c, int64_t ldc, int64_t M,
-                               int64_t N, int64_t K, const void* bias, int32_t bias_mode,
+                               int64_t N, int64_t K, int32_t batch, int64_t a_batch_stride,
+                               int64_t c_batch_stride, const void* bias, int32_t bias_mode,
                                int32_t activation, int32_t accumulate, int32_t dtype,
                                dsp_stream_t stream) {
   DSP_HOST_CHECK(a && bt && c && a_segment_offsets, DSP_EINVAL);
@@ -235,17 +240,19 @@ extern "C" int dsp_kv_map_gemm(const void* a, const int64_t* a_segment_offsets,
                      (activation == 0 || activation == 1),
                  DSP_EINVAL);
   DSP_HOST_CHECK(dtype == DSP_BF16, DSP_EUNSUPPORTED);
-  if (M == 0 || N == 0) return DSP_OK;
+  DSP_HOST_CHECK(batch >= 0 && batch <= 65535 && a_batch_stride >= 0 && c_batch_stride >= 0,
+                 DSP_EINVAL);
+  if (M == 0 || N == 0 || batch == 0) return DSP_OK;
   SegOffsets seg{};
   bool vec = dsp_aligned(a, 16) && dsp_aligned(bt, 16) && segment_len % BK == 0 &&
-             lda % 8 == 0 && ldb % 8 == 0;
+             lda % 8 == 0 && ldb % 8 == 0 && a_batch_stride % 8 == 0;
   for (int i = 0; i < num_segments; ++i) {
     seg.off[i] = a_segment_offsets[i];
     vec = vec && (seg.off[i] % 8 == 0);
   }
   const int64_t gm = (M + BM - 1) / BM, gn = (N + BN - 1) / BN;
   DSP_HOST_CHECK(gm < (int64_t(1) << 31) && gn <= 65535, DSP_EINVAL);
-  dim3 grid(static_cast<unsigned>(gn), static_cast<unsigned>(gm));
+  dim3 grid(static_cast<unsigned>(gn), static_cast<unsigned>(gm), static_cast<unsigned>(batch));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* ah = static_cast<const uint16_t*>(a);
   const uint16_t* bh = static_cast<const uint16_t*>(bt);
@@ -253,11 +260,12 @@ extern "C" int dsp_kv_map_gemm(const void* a, const int64_t* a_segment_offsets,
   const uint16_t* biash = static_cast<const uint16_t*>(bias);
   if (vec)
     map_gemm_kernel<true><<<grid, kThreads, 0, s>>>(ah, seg, segment_len, lda, bh, ldb, ch, ldc, M,
-                                                    N, K, biash, bias_mode, activation, accumulate);
+                                                    N, K, biash, bias_mode, activation, accumulate,
+                                                    a_batch_stride, c_batch_stride);
   else
     map_gemm_kernel<false><<<grid, kThreads, 0, s>>>(ah, seg, segment_len, lda, bh, ldb, ch, ldc,
                                                      M, N, K, biash, bias_mode, activation,
-                                                     accumulate);
+                                                     accumulate, a_batch_stride, c_batch_stride);
   return dsp_launch_status();
 }
 

@@ -278,12 +278,13 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
 // One wave per (sequence, head), four heads per workgroup: grid = (ceil(Hq/4), B).
 // Lanes first run over partitions (max of m, partition weights 2^(m_p - M), and their
 // l-weighted sum), the weights go through the wave's LDS row, then lanes run over dims
-// and stream the partial accumulators with independent loads.
-template <typename Tag>
+// and stream the partial accumulators, eight partitions' loads issued before their FMAs.
+template <typename Tag, int D>
 __global__ __launch_bounds__(256) void decode_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
-    const int32_t* __restrict__ ctx_lens, int32_t max_ctx, int32_t D, int32_t P,
-    int32_t num_parts, int32_t Hq, uint16_t* __restrict__ out, int64_t osb, int64_t osh) {
+    const int32_t* __restrict__ ctx_lens, int32_t max_ctx, int32_t P, int32_t num_parts,
+    int32_t Hq, uint16_t* __restrict__ out, int64_t osb, int64_t osh) {
+  constexpr int NV = D > 64 ? 2 : 1;  // dims per lane: lane, lane + 64
   __shared__ float s_w[4][64];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h = blockIdx.x * 4 + wave, b = blockIdx.y;
@@ -298,7 +299,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(
 #pragma unroll
   for (int mask = 1; mask < 64; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
   const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f, A0 = 0.f, A1 = 0.f;  // dims lane and lane + 64 (D <= 128)
+  const bool act = lane < D;
+  float L = 0.f, A[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) A[j] = 0.f;
   for (int p0 = 0; p0 < nparts; p0 += 64) {
     const int p = p0 + lane;
     float w = 0.f;
@@ -311,12 +315,25 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int np = min(64, nparts - p0);
-    const float* src = ws_acc + (row0 + p0) * D;
-#pragma unroll 8
-    for (int k = 0; k < np; ++k) {
+    const float* src = ws_acc + (row0 + p0) * D + (act ? lane : 0);
+    int k = 0;
+    for (; k + 8 <= np; k += 8) {
+      float v[8][NV];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) v[u][j] = src[int64_t(k + u) * D + 64 * j];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wk = s_w[wave][k + u];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) A[j] = fmaf(v[u][j], wk, A[j]);
+      }
+    }
+    for (; k < np; ++k) {
       const float wk = s_w[wave][k];
-      if (lane < D) A0 = fmaf(src[int64_t(k) * D + lane], wk, A0);
-      if (lane + 64 < D) A1 = fmaf(src[int64_t(k) * D + lane + 64], wk, A1);
+#pragma unroll
+      for (int j = 0; j < NV; ++j) A[j] = fmaf(src[int64_t(k) * D + 64 * j], wk, A[j]);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -326,8 +343,22 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(
   for (int mask = 1; mask < 64; mask <<= 1) L += dsp_shfl_xor(L, mask);
   const float inv = L > 0.f ? 1.f / L : 0.f;
   uint16_t* o = out + int64_t(b) * osb + int64_t(h) * osh;
-  if (lane < D) o[lane] = narrow<Tag>(A0 * inv);
-  if (lane + 64 < D) o[lane + 64] = narrow<Tag>(A1 * inv);
+  if (act) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) o[lane + 64 * j] = narrow<Tag>(A[j] * inv);
+  }
+}
+
+template <typename Tag>
+void launch_combine(int D, dim3 grid, hipStream_t s, const float* ws_acc, const float* ws_ml,
+                    const int32_t* ctx_lens, int32_t max_ctx, int32_t P, int32_t num_parts,
+                    int32_t Hq, uint16_t* out, int64_t osb, int64_t osh) {
+  switch (D) {
+    case 16: decode_combine_kernel<Tag, 16><<<grid, 256, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, P, num_parts, Hq, out, osb, osh); break;
+    case 32: decode_combine_kernel<Tag, 32><<<grid, 256, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, P, num_parts, Hq, out, osb, osh); break;
+    case 64: decode_combine_kernel<Tag, 64><<<grid, 256, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, P, num_parts, Hq, out, osb, osh); break;
+    default: decode_combine_kernel<Tag, 128><<<grid, 256, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, P, num_parts, Hq, out, osb, osh); break;
+  }
 }
 
 int wg_step_for(int D) {
@@ -474,10 +505,10 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   if (st != DSP_OK || num_parts <= 1) return st;
   dim3 cgrid(static_cast<unsigned>((Hq + 3) / 4), static_cast<unsigned>(B));
   if (dtype == DSP_BF16)
-    decode_combine_kernel<Bf16Tag><<<cgrid, 256, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, D, P,
-                                                         num_parts, Hq, oh, o_stride_b, o_stride_h);
+    launch_combine<Bf16Tag>(D, cgrid, s, ws_acc, ws_ml, ctx_lens, max_ctx, P, num_parts, Hq, oh,
+                            o_stride_b, o_stride_h);
   else
-    decode_combine_kernel<F16Tag><<<cgrid, 256, 0, s>>>(ws_acc, ws_ml, ctx_lens, max_ctx, D, P,
-                                                        num_parts, Hq, oh, o_stride_b, o_stride_h);
+    launch_combine<F16Tag>(D, cgrid, s, ws_acc, ws_ml, ctx_lens, max_ctx, P, num_parts, Hq, oh,
+                           o_stride_b, o_stride_h);
   return dsp_launch_status();
 }

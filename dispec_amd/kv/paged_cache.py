@@ -238,6 +238,37 @@ class PagedKVCache:
         v = v.to(device=self.key.device, dtype=self.dtype)
         self.import_batch([block_ids], k, v, [0, k.shape[1]])
 
+    # -- device-table forms (no host round trip; what graph-captured callers use) ---------
+    def gather_into(self, block_table: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
+                    k_buf: torch.Tensor, v_buf: torch.Tensor) -> None:
+        """export_batch with the int32 block table and int64 token offsets already on the
+        GPU; k_buf/v_buf hold num_layers * cu_seqlens[-1] contiguous rows."""
+        _lib.check(_lib.lib().dsp_kv_gather(
+            self.key.data_ptr(), self.value.data_ptr(), self.num_layers, self.layer_bytes,
+            self.num_blocks, self.row_bytes, self.block_size, block_table.data_ptr(),
+            block_table.stride(0), cu_seqlens.data_ptr(), block_table.shape[0], int(max_seqlen),
+            k_buf.data_ptr(), v_buf.data_ptr(), self._err.data_ptr(), self._stream()),
+            "dsp_kv_gather")
+
+    def scatter_from(self, block_table: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
+                     k_buf: torch.Tensor, v_buf: torch.Tensor) -> None:
+        """import_batch with device-side tables (the inverse of gather_into)."""
+        _lib.check(_lib.lib().dsp_kv_scatter(
+            self.key.data_ptr(), self.value.data_ptr(), self.num_layers, self.layer_bytes,
+            self.num_blocks, self.row_bytes, self.block_size, block_table.data_ptr(),
+            block_table.stride(0), cu_seqlens.data_ptr(), block_table.shape[0], int(max_seqlen),
+            k_buf.data_ptr(), v_buf.data_ptr(), self._err.data_ptr(), self._stream()),
+            "dsp_kv_scatter")
+
+    def copy_blocks_device(self, src: "PagedKVCache", src_ids: torch.Tensor,
+                           dst_ids: torch.Tensor) -> None:
+        """Block copy src -> self with int32 id arrays already on the GPU."""
+        _lib.check(_lib.lib().dsp_kv_copy_blocks(
+            src.key.data_ptr(), src.value.data_ptr(), src.layer_bytes, src.num_blocks,
+            self.key.data_ptr(), self.value.data_ptr(), self.layer_bytes, self.num_blocks,
+            self.num_layers, self.block_bytes, src_ids.data_ptr(), dst_ids.data_ptr(),
+            src_ids.numel(), self._err.data_ptr(), self._stream()), "dsp_kv_copy_blocks")
+
     # -- block copies (copy-on-write, prefix-cache spill) ----------------------------------
     def copy_blocks_from(self, src: "PagedKVCache", src_ids: list[int], dst_ids: list[int]) -> None:
         """dst[l, block d] = src[l, block s] for every layer, K and V."""

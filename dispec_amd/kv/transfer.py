@@ -20,6 +20,7 @@ transposed once at load so both GEMM operands are read along K.
 
 from __future__ import annotations
 
+import ctypes
 import json
 import warnings
 from dataclasses import dataclass, field
@@ -81,19 +82,22 @@ def apply_rope(keys: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torc
 # -- the GEMM --------------------------------------------------------------------------------
 def _gemm(a: torch.Tensor, seg_offsets: list[int], seg_len: int, lda: int, M: int,
           bt: torch.Tensor, out: torch.Tensor, bias: torch.Tensor | None = None,
-          bias_mode: int = 0, act: int = 0, accumulate: bool = False) -> torch.Tensor:
-    """out[M, N] = epilogue(A . bt^T); A's column k is a[seg_offsets[k // seg_len] + m*lda
-    + k % seg_len]; bt is (N, K) with K contiguous."""
+          bias_mode: int = 0, act: int = 0, accumulate: bool = False, batch: int = 1,
+          a_batch_stride: int = 0, c_batch_stride: int = 0) -> torch.Tensor:
+    """out[z, M, N] = epilogue(A_z . bt^T) for z < batch; A_z's column k is
+    a[z*a_batch_stride + seg_offsets[k // seg_len] + m*lda + k % seg_len]; bt is (N, K) with
+    K contiguous; out's rows are out.stride(-2) apart, problems c_batch_stride apart."""
     N, K = bt.shape
     if bt.stride(1) != 1:
         raise ValueError("Bt must be K-contiguous")
-    if out.stride(1) != 1 or tuple(out.shape) != (M, N):
-        raise ValueError(f"out must be a row-major ({M}, {N}) view")
-    offs = (_lib.c_int64 * len(seg_offsets))(*seg_offsets)
+    if out.stride(-1) != 1 or tuple(out.shape[-2:]) != (M, N):
+        raise ValueError(f"out must be row-major (..., {M}, {N})")
+    offs = (ctypes.c_int64 * len(seg_offsets))(*seg_offsets)
     _lib.check(_lib.lib().dsp_kv_map_gemm(
         a.data_ptr(), offs, len(seg_offsets), seg_len, lda, bt.data_ptr(), bt.stride(0),
-        out.data_ptr(), out.stride(0), M, N, K, _lib.ptr(bias), bias_mode, act, int(accumulate),
-        _lib.DSP_BF16, _lib.stream_of(out)), "dsp_kv_map_gemm")
+        out.data_ptr(), out.stride(-2), M, N, K, batch, a_batch_stride, c_batch_stride,
+        _lib.ptr(bias), bias_mode, act, int(accumulate), _lib.DSP_BF16, _lib.stream_of(out)),
+        "dsp_kv_map_gemm")
     return out
 
 
@@ -149,22 +153,29 @@ class LayerMap:
         self._kernel_ready = True
 
     def apply_into(self, a: torch.Tensor, seg_offsets: list[int], seg_len: int, lda: int,
-                   rows: int, out: torch.Tensor, use_residual: bool = True) -> torch.Tensor:
-        """out (rows, N) = x @ W + b (+ residual) with x's design rows read in place."""
+                   rows: int, out: torch.Tensor, use_residual: bool = True, batch: int = 1,
+                   a_batch_stride: int = 0, c_batch_stride: int = 0) -> torch.Tensor:
+        """out (rows, N) = x @ W + b (+ residual) with x's design rows read in place; with
+        batch > 1, `batch` problems a_batch_stride / c_batch_stride elements apart."""
         self._prepare()
+        bs = dict(batch=batch, a_batch_stride=a_batch_stride, c_batch_stride=c_batch_stride)
         if self.factors is not None:
             r = self._lt.shape[0]
-            tmp = torch.empty((rows, r), dtype=torch.bfloat16, device=out.device)
-            _gemm(a, seg_offsets, seg_len, lda, rows, self._lt, tmp)
-            _gemm(tmp, [0], r, r, rows, self._rt, out, self._b, bias_mode=1)
+            tmp = torch.empty((batch, rows, r), dtype=torch.bfloat16, device=out.device)
+            _gemm(a, seg_offsets, seg_len, lda, rows, self._lt, tmp, batch=batch,
+                  a_batch_stride=a_batch_stride, c_batch_stride=rows * r)
+            _gemm(tmp, [0], r, r, rows, self._rt, out, self._b, bias_mode=1, batch=batch,
+                  a_batch_stride=rows * r, c_batch_stride=c_batch_stride)
         else:
-            _gemm(a, seg_offsets, seg_len, lda, rows, self._wt, out, self._b, bias_mode=1)
+            _gemm(a, seg_offsets, seg_len, lda, rows, self._wt, out, self._b, bias_mode=1, **bs)
         if use_residual and self.residual is not None:
             down_w, down_b = self._down
-            hidden = torch.empty((rows, down_w.shape[0]), dtype=torch.bfloat16, device=out.device)
-            _gemm(a, seg_offsets, seg_len, lda, rows, down_w, hidden, down_b, bias_mode=2, act=1)
-            _gemm(hidden, [0], hidden.shape[1], hidden.shape[1], rows, self._up, out,
-                  accumulate=True)
+            hid = down_w.shape[0]
+            hidden = torch.empty((batch, rows, hid), dtype=torch.bfloat16, device=out.device)
+            _gemm(a, seg_offsets, seg_len, lda, rows, down_w, hidden, down_b, bias_mode=2, act=1,
+                  batch=batch, a_batch_stride=a_batch_stride, c_batch_stride=rows * hid)
+            _gemm(hidden, [0], hid, hid, rows, self._up, out, accumulate=True, batch=batch,
+                  a_batch_stride=rows * hid, c_batch_stride=c_batch_stride)
         return out
 
     def apply(self, x: torch.Tensor, use_residual: bool = True) -> torch.Tensor:

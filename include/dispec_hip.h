@@ -195,6 +195,9 @@ int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
  *   Bt         : N x K row-major (K contiguous), leading dimension ldb: W^T for
  *                x @ W, or an F.linear weight as stored.
  *   C          : M x N row-major, leading dimension ldc.
+ *   batch      : independent problems sharing Bt and the bias (grid z, <= 65535); problem
+ *                z reads A at a + z*a_batch_stride and writes C at c + z*c_batch_stride
+ *                (elements) -- e.g. several requests' transport buffers at once.
  *   bias_mode  : 0 none, 1 bf16(bf16(acc) + b) (x @ W + b as two bf16 ops),
  *                2 bf16(acc + b) (F.linear / addmm).  bias is bf16 [N].
  *   activation : 0 none, 1 gelu (erf form) applied to the rounded value and rounded.
@@ -202,7 +205,8 @@ int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
  * dtype: DSP_BF16. */
 int dsp_kv_map_gemm(const void* a, const int64_t* a_segment_offsets, int32_t num_segments,
                     int64_t segment_len, int64_t lda, const void* bt, int64_t ldb, void* c,
-                    int64_t ldc, int64_t M, int64_t N, int64_t K, const void* bias,
+                    int64_t ldc, int64_t M, int64_t N, int64_t K, int32_t batch,
+                    int64_t a_batch_stride, int64_t c_batch_stride, const void* bias,
                     int32_t bias_mode, int32_t activation, int32_t accumulate, int32_t dtype,
                     dsp_stream_t stream);
 
