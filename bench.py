@@ -405,6 +405,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-aux", action="store_true")
+    ap.add_argument("--only", default="",
+                    help="comma list of c2,c4,c5: run just these auxiliary configs and print "
+                         "their numbers (no headline line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the KV data path has no cross-GPU exchange in "
@@ -416,11 +419,22 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     torch.cuda.set_device(0)
+    configs = (("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5))
+    if args.only:
+        want = set(args.only.split(","))
+        aux = {}
+        for name, fn in configs:
+            if name in want:
+                _log(f"config {name[1:]}")
+                aux.update(fn(torch))
+        print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v)
+                          for k, v in aux.items()}), flush=True)
+        return 0
     dec = bench_decode(torch, args.steps, args.warmup)
     aux = {}
     if not args.no_aux:
-        for name, fn in (("config 2", bench_c2), ("config 4", bench_c4), ("config 5", bench_c5)):
-            _log(f"{name}")
+        for name, fn in configs:
+            _log(f"config {name[1:]}")
             aux.update(fn(torch))
     cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)
     line = {

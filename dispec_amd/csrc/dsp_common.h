@@ -40,12 +40,23 @@ static inline int dsp_vec_width(std::initializer_list<int64_t> vals) {
 
 // ---------------------------------------------------------------- device helpers
 // Byte vectors used for coalesced copies.  16 B per lane is one global_load_dwordx4.
+// Native clang vectors, not HIP's uint4/uint2 structs: conditional loads of the struct
+// types do not if-convert and serialise behind per-load waits.
+typedef uint32_t dsp_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t dsp_u32x2 __attribute__((ext_vector_type(2)));
 template <int VEC> struct dsp_vec;
-template <> struct dsp_vec<16> { using type = uint4; };
-template <> struct dsp_vec<8> { using type = uint2; };
+template <> struct dsp_vec<16> { using type = dsp_u32x4; };
+template <> struct dsp_vec<8> { using type = dsp_u32x2; };
 template <> struct dsp_vec<4> { using type = uint32_t; };
 template <> struct dsp_vec<2> { using type = uint16_t; };
 template <> struct dsp_vec<1> { using type = uint8_t; };
+
+// Streaming (non-temporal) load/store for data touched once: keeps the copy out of the
+// caches' way.
+template <typename V>
+__device__ __forceinline__ V dsp_ld_stream(const V* p) { return __builtin_nontemporal_load(p); }
+template <typename V>
+__device__ __forceinline__ void dsp_st_stream(V v, V* p) { __builtin_nontemporal_store(v, p); }
 
 // bf16 / fp16 <-> fp32.  bf16 widening is exact (a shift); narrowing rounds to nearest
 // even, as torch's .to(torch.bfloat16) does (NaN kept quiet).

@@ -30,25 +30,23 @@ __global__ __launch_bounds__(kThreads) void slot_rows_kernel(
   }
   char* dense = const_cast<char*>(blockIdx.y == 0 ? k : v) + row * src_stride;
   char* pooled = (blockIdx.y == 0 ? k_pool : v_pool) + slot * pool_stride;
-  const char* src = kScatter ? dense : pooled;
-  char* dst = kScatter ? pooled : dense;
+  const V* src = reinterpret_cast<const V*>(kScatter ? dense : pooled);
+  V* dst = reinterpret_cast<V*>(kScatter ? pooled : dense);
   constexpr int U = 4;
-  for (int c0 = lane; c0 < chunks_per_row; c0 += U * lanes_per_row) {
+  int c = lane;
+  // Full rounds: U vectors per lane, all loads issued before the stores.
+  for (; c + (U - 1) * lanes_per_row < chunks_per_row; c += U * lanes_per_row) {
     V buf[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + u * lanes_per_row;
-      if (c < chunks_per_row) buf[u] = reinterpret_cast<const V*>(src)[c];
-    }
+    for (int u = 0; u < U; ++u) buf[u] = dsp_ld_stream(src + c + u * lanes_per_row);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int c = c0 + u * lanes_per_row;
-      if (c < chunks_per_row) reinterpret_cast<V*>(dst)[c] = buf[u];
-    }
+    for (int u = 0; u < U; ++u) dsp_st_stream(buf[u], dst + c + u * lanes_per_row);
   }
+  for (; c < chunks_per_row; c += lanes_per_row) dsp_st_stream(dsp_ld_stream(src + c), dst + c);
 }
 
-// Copy `bytes` (a multiple of VEC) from src to dst with the whole workgroup.
+// Copy `bytes` (a multiple of VEC) from src to dst with the whole workgroup: full rounds
+// of U vectors per thread (loads first, no per-vector guards), then a guarded tail.
 template <int VEC>
 __device__ __forceinline__ void wg_copy(const char* __restrict__ src, char* __restrict__ dst,
                                         int64_t bytes) {
@@ -57,19 +55,15 @@ __device__ __forceinline__ void wg_copy(const char* __restrict__ src, char* __re
   const int64_t n = bytes / VEC;
   const V* s = reinterpret_cast<const V*>(src);
   V* d = reinterpret_cast<V*>(dst);
-  for (int64_t i0 = threadIdx.x; i0 < n; i0 += int64_t(U) * kThreads) {
+  int64_t i0 = threadIdx.x;
+  for (; i0 + int64_t(U - 1) * kThreads < n; i0 += int64_t(U) * kThreads) {
     V buf[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = i0 + int64_t(u) * kThreads;
-      if (i < n) buf[u] = s[i];
-    }
+    for (int u = 0; u < U; ++u) buf[u] = dsp_ld_stream(s + i0 + u * kThreads);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t i = i0 + int64_t(u) * kThreads;
-      if (i < n) d[i] = buf[u];
-    }
+    for (int u = 0; u < U; ++u) dsp_st_stream(buf[u], d + i0 + u * kThreads);
   }
+  for (; i0 < n; i0 += kThreads) dsp_st_stream(dsp_ld_stream(s + i0), d + i0);
 }
 
 // ------------------------------------------------------------------------------- J2

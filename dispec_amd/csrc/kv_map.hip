@@ -54,13 +54,13 @@ __device__ __forceinline__ float bf16_round(float x) {
 // and `k` is the column inside it.  Otherwise column k is element k % seg_len of
 // segment k / seg_len and each element is fetched on its own (small, unaligned maps).
 template <bool kVec>
-__device__ __forceinline__ uint4 load_chunk(const uint16_t* __restrict__ base,
+__device__ __forceinline__ dsp_u32x4 load_chunk(const uint16_t* __restrict__ base,
                                             const SegOffsets& seg, int64_t seg_len, int64_t ld,
                                             int64_t row, int64_t rows, int64_t k, int64_t kabs,
                                             int64_t K) {
-  if (row >= rows || kabs >= K) return make_uint4(0, 0, 0, 0);
+  if (row >= rows || kabs >= K) return dsp_u32x4{0u, 0u, 0u, 0u};
   if constexpr (kVec) {
-    return *reinterpret_cast<const uint4*>(base + k + row * ld);
+    return *reinterpret_cast<const dsp_u32x4*>(base + k + row * ld);
   } else {
     uint16_t e[8];
 #pragma unroll
@@ -69,8 +69,8 @@ __device__ __forceinline__ uint4 load_chunk(const uint16_t* __restrict__ base,
       const int64_t s = kk / seg_len;
       e[i] = kk < K ? base[seg.off[s] + (kk - s * seg_len) + row * ld] : uint16_t(0);
     }
-    return make_uint4(uint32_t(e[0]) | (uint32_t(e[1]) << 16), uint32_t(e[2]) | (uint32_t(e[3]) << 16),
-                      uint32_t(e[4]) | (uint32_t(e[5]) << 16), uint32_t(e[6]) | (uint32_t(e[7]) << 16));
+    return dsp_u32x4{uint32_t(e[0]) | (uint32_t(e[1]) << 16), uint32_t(e[2]) | (uint32_t(e[3]) << 16),
+                      uint32_t(e[4]) | (uint32_t(e[5]) << 16), uint32_t(e[6]) | (uint32_t(e[7]) << 16)};
   }
 }
 
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kThreads) void map_gemm_kernel(
   // Each thread stages 2 chunks of A and 2 of Bt per K step: rows tid/4 and tid/4 + 64,
   // chunk tid % 4 (8 elements) of the 32-wide K slice.
   const int lr = tid >> 2, lc = (tid & 3) * 8;
-  uint4 ra[2], rb[2];
+  dsp_u32x4 ra[2], rb[2];
   SegOffsets b_seg{};
   auto fetch = [&](int64_t k0) {
     // k0 is uniform across the workgroup, so the segment lookup stays scalar.
@@ -108,8 +108,8 @@ __global__ __launch_bounds__(kThreads) void map_gemm_kernel(
   auto stash = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      *reinterpret_cast<uint4*>(&sa[buf][lr + 64 * i][lc]) = ra[i];
-      *reinterpret_cast<uint4*>(&sb[buf][lr + 64 * i][lc]) = rb[i];
+      *reinterpret_cast<dsp_u32x4*>(&sa[buf][lr + 64 * i][lc]) = ra[i];
+      *reinterpret_cast<dsp_u32x4*>(&sb[buf][lr + 64 * i][lc]) = rb[i];
     }
   };
 
@@ -127,11 +127,11 @@ __global__ __launch_bounds__(kThreads) void map_gemm_kernel(
   for (int64_t kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nk) fetch((kt + 1) * BK);
-    uint4 fa[4], fb[4];
+    dsp_u32x4 fa[4], fb[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      fa[i] = *reinterpret_cast<const uint4*>(&sa[buf][wm + 16 * i + fr][fk]);
-      fb[i] = *reinterpret_cast<const uint4*>(&sb[buf][wn + 16 * i + fr][fk]);
+      fa[i] = *reinterpret_cast<const dsp_u32x4*>(&sa[buf][wm + 16 * i + fr][fk]);
+      fb[i] = *reinterpret_cast<const dsp_u32x4*>(&sb[buf][wn + 16 * i + fr][fk]);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -176,8 +176,8 @@ __global__ __launch_bounds__(kThreads) void map_gemm_kernel(
         if (!full) dst[e] = ybits[e];
       }
       if (full)
-        *reinterpret_cast<uint2*>(dst) = make_uint2(uint32_t(ybits[0]) | (uint32_t(ybits[1]) << 16),
-                                                    uint32_t(ybits[2]) | (uint32_t(ybits[3]) << 16));
+        *reinterpret_cast<dsp_u32x2*>(dst) = dsp_u32x2{uint32_t(ybits[0]) | (uint32_t(ybits[1]) << 16),
+                                                    uint32_t(ybits[2]) | (uint32_t(ybits[3]) << 16)};
     }
   }
 }

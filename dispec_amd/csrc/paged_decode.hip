@@ -135,10 +135,10 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
   const int rg = lane / RL;  // row group: which row of a load this lane reads
   const int c = lane % RL;   // 16-byte chunk of the row: dims [8c, 8c+8)
 
-  uint4 qv[G];
+  dsp_u32x4 qv[G];
 #pragma unroll
   for (int g = 0; g < G; ++g)
-    qv[g] = *reinterpret_cast<const uint4*>(q + int64_t(b) * qsb + int64_t(kvh * G + g) * qsh + 8 * c);
+    qv[g] = *reinterpret_cast<const dsp_u32x4*>(q + int64_t(b) * qsb + int64_t(kvh * G + g) * qsh + 8 * c);
 
   float m[G], l[G], acc[G][8];
 #pragma unroll
@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
 
   const int64_t head_off = int64_t(kvh) * kvs_head + 8 * c;
   for (int base = wave * Gm::kStep; base < n; base += Gm::kWgStep) {
-    uint4 kr[TPL], vr[TPL];
+    dsp_u32x4 kr[TPL], vr[TPL];
     bool valid[TPL];
 #pragma unroll
     for (int i = 0; i < TPL; ++i) {
@@ -160,11 +160,11 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
       valid[i] = slot >= 0;
       const int64_t off = int64_t(valid[i] ? slot : 0) * kvs_slot + head_off;
       if (valid[i]) {
-        kr[i] = *reinterpret_cast<const uint4*>(kc + off);
-        vr[i] = *reinterpret_cast<const uint4*>(vc + off);
+        kr[i] = *reinterpret_cast<const dsp_u32x4*>(kc + off);
+        vr[i] = *reinterpret_cast<const dsp_u32x4*>(vc + off);
       } else {
-        kr[i] = make_uint4(0, 0, 0, 0);
-        vr[i] = make_uint4(0, 0, 0, 0);
+        kr[i] = dsp_u32x4{0u, 0u, 0u, 0u};
+        vr[i] = dsp_u32x4{0u, 0u, 0u, 0u};
       }
     }
     float s[TPL][G];

@@ -36,7 +36,7 @@ struct Bf16Tag {};
 struct F16Tag {};
 
 template <typename Tag>
-__device__ __forceinline__ f32x4 mfma32(uint4 a, uint4 b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma32(dsp_u32x4 a, dsp_u32x4 b, f32x4 c) {
   if constexpr (std::is_same<Tag, Bf16Tag>::value)
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -110,12 +110,12 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   const int64_t bt_row = int64_t(b) * bt_stride;
   const int64_t head_off = int64_t(kvh) * kvs_head;
 
-  uint4 qop[NKK];
+  dsp_u32x4 qop[NKK];
 #pragma unroll
   for (int kk = 0; kk < NKK; ++kk) {
-    qop[kk] = row_ok ? *reinterpret_cast<const uint4*>(q + int64_t(q0 + qi) * qst + int64_t(h) * qsh +
+    qop[kk] = row_ok ? *reinterpret_cast<const dsp_u32x4*>(q + int64_t(q0 + qi) * qst + int64_t(h) * qsh +
                                                        32 * kk + 8 * grp)
-                     : make_uint4(0, 0, 0, 0);
+                     : dsp_u32x4{0u, 0u, 0u, 0u};
   }
 
   float m = -INFINITY, lpart = 0.f;
@@ -125,31 +125,31 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
 
   for (int t0 = wave * 32; t0 < kend; t0 += 32 * kWaves) {
     // K operands of the two 16-key halves: lane holds key t0 + 16*st + n, dims 8*grp+32*kk.
-    uint4 kop[2][NKK];
+    dsp_u32x4 kop[2][NKK];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const int key = t0 + 16 * st + n;
       const int64_t s = key < kend ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk)
-        kop[st][kk] = s >= 0 ? *reinterpret_cast<const uint4*>(kc + s * kvs_slot + head_off +
+        kop[st][kk] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(kc + s * kvs_slot + head_off +
                                                                 32 * kk + 8 * grp)
-                             : make_uint4(0, 0, 0, 0);
+                             : dsp_u32x4{0u, 0u, 0u, 0u};
     }
     // Stage this step's 32 V rows in the wave's LDS slab (zeros past kend).
-    uint4 vst[VPL];
+    dsp_u32x4 vst[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int idx = lane + 64 * i;
       const int key = t0 + idx / CPR;
       const int64_t s = key < kend ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
-      vst[i] = s >= 0 ? *reinterpret_cast<const uint4*>(vc + s * kvs_slot + head_off + 8 * (idx % CPR))
-                      : make_uint4(0, 0, 0, 0);
+      vst[i] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(vc + s * kvs_slot + head_off + 8 * (idx % CPR))
+                      : dsp_u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int idx = lane + 64 * i;
-      *reinterpret_cast<uint4*>(&s_v[wave][idx / CPR][8 * (idx % CPR)]) = vst[i];
+      *reinterpret_cast<dsp_u32x4*>(&s_v[wave][idx / CPR][8 * (idx % CPR)]) = vst[i];
     }
 
     f32x4 sc[2];
@@ -190,8 +190,8 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
       }
     }
     lpart = lpart * alpha + psum;
-    const uint4 pop = make_uint4(pack2(pb[0], pb[1]), pack2(pb[2], pb[3]), pack2(pb[4], pb[5]),
-                                 pack2(pb[6], pb[7]));
+    const dsp_u32x4 pop = dsp_u32x4{pack2(pb[0], pb[1]), pack2(pb[2], pb[3]), pack2(pb[4], pb[5]),
+                                 pack2(pb[6], pb[7])};
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[nt] *= alpha;
 
@@ -208,8 +208,8 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
         const int kl = u < 4 ? 4 * grp + u : 16 + 4 * grp + (u - 4);
         v[u] = s_v[wave][kl][d];
       }
-      const uint4 vop = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]),
-                                   pack2(v[6], v[7]));
+      const dsp_u32x4 vop = dsp_u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]),
+                                   pack2(v[6], v[7])};
       acc[nt] = mfma32<Tag>(vop, pop, acc[nt]);
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
