@@ -27,6 +27,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxParts = 64;  // key partitions per tile the merge kernel accepts
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -71,8 +72,9 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
     const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
-    int32_t G, float scale_log2, uint16_t* __restrict__ out, int64_t ost, int64_t osh,
-    int32_t* __restrict__ err_count) {
+    int32_t G, float scale_log2, int32_t P, int32_t num_parts, int32_t tiles_max,
+    float* __restrict__ ws_acc, float* __restrict__ ws_ml, uint16_t* __restrict__ out,
+    int64_t ost, int64_t osh, int32_t* __restrict__ err_count) {
   constexpr int NKK = D / 32;        // 32-dim K steps of the score MFMA
   constexpr int NT = D / 16;         // 16-dim output tiles
   constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
@@ -84,7 +86,9 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   __shared__ float s_l[kWaves][16];
   __shared__ float s_acc[kWaves][16][D + 1];
 
-  const int tile = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int part = blockIdx.x % num_parts, tile = blockIdx.x / num_parts;
+  const int kvh = blockIdx.y, b = blockIdx.z;
+  const int KVH = gridDim.y;
   const int q0 = cu_q[b];
   const int qlen = cu_q[b + 1] - q0;
   int ctx = ctx_lens[b];
@@ -93,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   if (qlen <= 0 || r0 >= rows) return;
   const bool bad = ctx > max_ctx || ctx < qlen;
   if (bad) {
-    if (threadIdx.x == 0 && tile == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
+    if (threadIdx.x == 0 && tile == 0 && part == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
     ctx = 0;  // no keys: rows are written as zeros
   }
 
@@ -107,6 +111,11 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   const int pos_q = ctx - qlen + qi;  // keys 0..pos_q are visible to this row
   const int r_last = min(r0 + 15, rows - 1);
   const int kend = bad ? 0 : ctx - qlen + r_last / G + 1;  // keys any row of the tile sees
+  // Split-K: this workgroup covers keys [kbeg, kfin) of the tile's causal range.
+  const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
+  if (part >= nparts) return;
+  const int kbeg = part * P;
+  const int kfin = min(kbeg + P, kend);
   const int64_t bt_row = int64_t(b) * bt_stride;
   const int64_t head_off = int64_t(kvh) * kvs_head;
 
@@ -123,13 +132,13 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int t0 = wave * 32; t0 < kend; t0 += 32 * kWaves) {
+  for (int t0 = kbeg + wave * 32; t0 < kfin; t0 += 32 * kWaves) {
     // K operands of the two 16-key halves: lane holds key t0 + 16*st + n, dims 8*grp+32*kk.
     dsp_u32x4 kop[2][NKK];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const int key = t0 + 16 * st + n;
-      const int64_t s = key < kend ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
+      const int64_t s = key < kfin ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk)
         kop[st][kk] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(kc + s * kvs_slot + head_off +
@@ -142,7 +151,7 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     for (int i = 0; i < VPL; ++i) {
       const int idx = lane + 64 * i;
       const int key = t0 + idx / CPR;
-      const int64_t s = key < kend ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
+      const int64_t s = key < kfin ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
       vst[i] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(vc + s * kvs_slot + head_off + 8 * (idx % CPR))
                       : dsp_u32x4{0u, 0u, 0u, 0u};
     }
@@ -245,8 +254,70 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
       L = fmaf(s_l[w][rr], e, L);
       A = fmaf(s_acc[w][rr][d], e, A);
     }
+    if (nparts == 1) {
+      const int qrow = q0 + row / G, hh = kvh * G + row % G;
+      out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(L > 0.f ? A / L : 0.f);
+    } else {
+      const int64_t slot = ((int64_t(b) * KVH + kvh) * tiles_max + tile) * num_parts + part;
+      ws_acc[(slot * 16 + rr) * D + d] = A;
+      if (d == 0) {
+        ws_ml[2 * (slot * 16 + rr)] = M;
+        ws_ml[2 * (slot * 16 + rr) + 1] = L;
+      }
+    }
+  }
+}
+
+// Merge the key partitions of one (tile, KV head, sequence): grid = (tiles, KVH, B).
+// Thread (row, dim) pairs; the partition weights 2^(m_p - M) are formed once per row in
+// LDS, then each pair streams its partial accumulators.
+template <typename Tag, int D>
+__global__ __launch_bounds__(256) void mq_combine_kernel(
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
+    int32_t G, int32_t P, int32_t num_parts, int32_t tiles_max, uint16_t* __restrict__ out,
+    int64_t ost, int64_t osh) {
+  __shared__ float s_w[16][kMaxParts];
+  __shared__ float s_inv[16];
+  const int tile = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, KVH = gridDim.y;
+  const int q0 = cu_q[b];
+  const int qlen = cu_q[b + 1] - q0;
+  const int ctx = ctx_lens[b];
+  const int rows = qlen * G;
+  const int r0 = tile * 16;
+  if (qlen <= 0 || r0 >= rows || ctx > max_ctx || ctx < qlen) return;
+  const int r_last = min(r0 + 15, rows - 1);
+  const int kend = ctx - qlen + r_last / G + 1;
+  const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
+  if (nparts <= 1) return;  // written directly by the attention kernel
+  const int64_t slot0 = ((int64_t(b) * KVH + kvh) * tiles_max + tile) * num_parts;
+  // weights: thread t handles row t / 16 and partitions t % 16, t % 16 + 16, ...
+  if (threadIdx.x < 256) {
+    const int rr = threadIdx.x >> 4, pl = threadIdx.x & 15;
+    float M = -INFINITY;
+    for (int p = pl; p < nparts; p += 16) M = fmaxf(M, ws_ml[2 * ((slot0 + p) * 16 + rr)]);
+#pragma unroll
+    for (int mask = 1; mask < 16; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float L = 0.f;
+    for (int p = pl; p < nparts; p += 16) {
+      const float w = dsp_exp2(ws_ml[2 * ((slot0 + p) * 16 + rr)] - Mu);
+      s_w[rr][p] = w;
+      L = fmaf(ws_ml[2 * ((slot0 + p) * 16 + rr) + 1], w, L);
+    }
+#pragma unroll
+    for (int mask = 1; mask < 16; mask <<= 1) L += dsp_shfl_xor(L, mask);
+    if (pl == 0) s_inv[rr] = L > 0.f ? 1.f / L : 0.f;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 16 * D; idx += 256) {
+    const int rr = idx / D, d = idx % D;
+    const int row = r0 + rr;
+    if (row >= rows) continue;
+    float A = 0.f;
+    for (int p = 0; p < nparts; ++p) A = fmaf(ws_acc[((slot0 + p) * 16 + rr) * D + d], s_w[rr][p], A);
     const int qrow = q0 + row / G, hh = kvh * G + row % G;
-    out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(L > 0.f ? A / L : 0.f);
+    out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(A * s_inv[rr]);
   }
 }
 
@@ -261,7 +332,46 @@ int launch_mq(int D, dim3 grid, hipStream_t s, A... args) {
   return dsp_launch_status();
 }
 
+template <typename Tag, typename... A>
+int launch_mq_combine(int D, dim3 grid, hipStream_t s, A... args) {
+  switch (D) {
+    case 32: mq_combine_kernel<Tag, 32><<<grid, 256, 0, s>>>(args...); break;
+    case 64: mq_combine_kernel<Tag, 64><<<grid, 256, 0, s>>>(args...); break;
+    default: mq_combine_kernel<Tag, 128><<<grid, 256, 0, s>>>(args...); break;
+  }
+  return dsp_launch_status();
+}
+
+int64_t mq_tiles(int32_t max_q_len, int32_t G) { return (int64_t(max_q_len) * G + 15) / 16; }
+
 }  // namespace
+
+extern "C" int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH,
+                                             int32_t max_q_len, int32_t max_ctx) {
+  if (B <= 0 || KVH <= 0 || Hq % KVH != 0 || max_q_len <= 0 || max_ctx <= 0) return 128;
+  const int64_t base = int64_t(B) * KVH * mq_tiles(max_q_len, Hq / KVH);
+  const int64_t whole = (int64_t(max_ctx) + 127) / 128 * 128;
+  if (base >= 1024) return static_cast<int32_t>(whole);
+  // Aim at ~2048 workgroups, partitions of at least 128 keys (one step of every wave).
+  int64_t want = (2048 + base - 1) / base;
+  if (want > kMaxParts) want = kMaxParts;
+  int64_t P = (max_ctx + want - 1) / want;
+  P = (P + 127) / 128 * 128;
+  if (P < 128) P = 128;
+  return static_cast<int32_t>(P < whole ? P : whole);
+}
+
+extern "C" size_t dsp_paged_mq_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
+                                               int32_t max_q_len, int32_t max_ctx,
+                                               int32_t partition_tokens) {
+  if (B <= 0 || KVH <= 0 || Hq % KVH != 0 || max_q_len <= 0 || max_ctx <= 0 ||
+      partition_tokens <= 0)
+    return 0;
+  const int64_t np = (int64_t(max_ctx) + partition_tokens - 1) / partition_tokens;
+  if (np <= 1) return 0;
+  return size_t(B) * KVH * mq_tiles(max_q_len, Hq / KVH) * np * 16 * (size_t(D) + 2) *
+         sizeof(float);
+}
 
 extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                                       const void* k_cache, const void* v_cache,
@@ -270,9 +380,11 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
                                       int64_t bt_stride, int32_t block_size,
                                       const int32_t* cu_q, const int32_t* ctx_lens, int32_t B,
                                       int32_t Hq, int32_t KVH, int32_t D, float scale,
-                                      int32_t max_q_len, int32_t max_ctx, void* out,
-                                      int64_t o_stride_t, int64_t o_stride_h, int32_t dtype,
-                                      int32_t* err_count, dsp_stream_t stream) {
+                                      int32_t max_q_len, int32_t max_ctx,
+                                      int32_t partition_tokens, void* workspace,
+                                      size_t workspace_bytes, void* out, int64_t o_stride_t,
+                                      int64_t o_stride_h, int32_t dtype, int32_t* err_count,
+                                      dsp_stream_t stream) {
   DSP_HOST_CHECK(q && k_cache && v_cache && block_table && cu_q && ctx_lens && out, DSP_EINVAL);
   DSP_HOST_CHECK(B >= 0 && B <= 65535 && Hq > 0 && KVH > 0 && KVH <= 65535 && Hq % KVH == 0 &&
                      max_q_len >= 0 && max_ctx >= 0 && num_slots >= 0,
@@ -287,9 +399,21 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
                      dsp_aligned(v_cache, 16),
                  DSP_EALIGN);
   const int G = Hq / KVH;
-  const int64_t tiles = (int64_t(max_q_len) * G + 15) / 16;
-  DSP_HOST_CHECK(tiles < (int64_t(1) << 31), DSP_EINVAL);
-  dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(KVH), static_cast<unsigned>(B));
+  const int64_t tiles = mq_tiles(max_q_len, G);
+  const int P = partition_tokens > 0
+                    ? partition_tokens
+                    : dsp_paged_mq_partition_tokens(B, Hq, KVH, max_q_len, max_ctx);
+  DSP_HOST_CHECK(P % 128 == 0, DSP_EINVAL);
+  const int num_parts = max_ctx > 0 ? (max_ctx + P - 1) / P : 1;
+  DSP_HOST_CHECK(num_parts <= kMaxParts, DSP_EINVAL);
+  DSP_HOST_CHECK(tiles * num_parts < (int64_t(1) << 31), DSP_EINVAL);
+  const size_t need = dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, max_q_len, max_ctx, P);
+  DSP_HOST_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr), DSP_EWORKSPACE);
+  DSP_HOST_CHECK(need == 0 || dsp_aligned(workspace, 16), DSP_EALIGN);
+  float* ws_acc = static_cast<float*>(workspace);
+  float* ws_ml = need ? ws_acc + int64_t(B) * KVH * tiles * num_parts * 16 * D : nullptr;
+  dim3 grid(static_cast<unsigned>(tiles * num_parts), static_cast<unsigned>(KVH),
+            static_cast<unsigned>(B));
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* qh = static_cast<const uint16_t*>(q);
@@ -297,13 +421,23 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
   const uint16_t* vh = static_cast<const uint16_t*>(v_cache);
   uint16_t* oh = static_cast<uint16_t*>(out);
   const int32_t lbs = dsp_log2i(block_size);
+  const int32_t tm = static_cast<int32_t>(tiles);
+  int st;
   if (dtype == DSP_BF16)
-    return launch_mq<Bf16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
-                              kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
-                              ctx_lens, max_ctx, G, scale_log2, oh, o_stride_t, o_stride_h,
-                              err_count);
-  return launch_mq<F16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
+    st = launch_mq<Bf16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
+                            kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
+                            ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, ws_acc, ws_ml,
+                            oh, o_stride_t, o_stride_h, err_count);
+  else
+    st = launch_mq<F16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
                            kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
-                           ctx_lens, max_ctx, G, scale_log2, oh, o_stride_t, o_stride_h,
-                           err_count);
+                           ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, ws_acc, ws_ml, oh,
+                           o_stride_t, o_stride_h, err_count);
+  if (st != DSP_OK || num_parts <= 1) return st;
+  dim3 cgrid(static_cast<unsigned>(tiles), static_cast<unsigned>(KVH), static_cast<unsigned>(B));
+  if (dtype == DSP_BF16)
+    return launch_mq_combine<Bf16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
+                                      num_parts, tm, oh, o_stride_t, o_stride_h);
+  return launch_mq_combine<F16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
+                                   num_parts, tm, oh, o_stride_t, o_stride_h);
 }

@@ -108,7 +108,7 @@ def paged_decode_attention_blocks(q, k_cache, v_cache, block_table, ctx_lens, kv
 
 def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_groups,
                        block_size=16, scale=None, max_q_len=None, max_ctx=None, out=None,
-                       err=None):
+                       err=None, partition_tokens=0, workspace=None):
     """Multi-query paged attention: speculative verify, chunked and fresh prefill.
 
     Per sequence b, rows q[cu_q[b]:cu_q[b+1]] are the last q_len_b tokens of a ctx_b-token
@@ -120,6 +120,8 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
     cu_q:        (B+1,) int32 query offsets;  ctx_lens: (B,) int32 context lengths
     max_q_len, max_ctx: host-side bounds (computed from cu_q / the table if omitted,
                  which costs a device->host copy)
+    partition_tokens: split-K key partition (0: chosen from the shape); workspace: an
+                 optional preallocated fp32 buffer for the partial results
     returns:     (sum q_len, num_heads, head_dim) in q's dtype
     """
     _lib.require_gpu(q, k_cache, v_cache, block_table, cu_q, ctx_lens)
@@ -151,10 +153,18 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
     out = torch.empty_like(q) if out is None else out
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
         raise ValueError("out must have q's shape and dtype with head_dim contiguous")
-    _lib.check(_lib.lib().dsp_paged_mq_attention(
+    L = _lib.lib()
+    P = partition_tokens or L.dsp_paged_mq_partition_tokens(B, Hq, KVH, int(max_q_len),
+                                                            int(max_ctx))
+    need = L.dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, int(max_q_len), int(max_ctx), P)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _lib.check(L.dsp_paged_mq_attention(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), S,
         k_cache.stride(0), k_cache.stride(1), block_table.data_ptr(), block_table.stride(0),
         block_size, cu_q.data_ptr(), ctx_lens.data_ptr(), B, Hq, KVH, D, float(scale),
-        int(max_q_len), int(max_ctx), out.data_ptr(), out.stride(0), out.stride(1),
-        _lib.dtype_code(q.dtype), _lib.ptr(err), _lib.stream_of(q)), "dsp_paged_mq_attention")
+        int(max_q_len), int(max_ctx), int(P), _lib.ptr(workspace), ws_bytes, out.data_ptr(),
+        out.stride(0), out.stride(1), _lib.dtype_code(q.dtype), _lib.ptr(err),
+        _lib.stream_of(q)), "dsp_paged_mq_attention")
     return out

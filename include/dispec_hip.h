@@ -172,16 +172,25 @@ int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  *   block_table: int32 [B, bt_stride] (power-of-two block_size).
  *   cu_q       : int32 [B+1] device offsets; ctx_lens: int32 [B], q_len_b <= ctx <= max_ctx.
  *   max_q_len  : upper bound of q_len_b (sizes the grid).
+ *   partition_tokens : split-K key partition (multiple of 128, at most 64 partitions of
+ *                max_ctx); 0 picks one from the shape.  More than one partition needs
+ *                `workspace` (dsp_paged_mq_workspace_bytes) and a merge kernel.
  * dtype DSP_BF16 / DSP_F16; D in {32, 64, 128}; any G = Hq / KVH.  A sequence with
  * q_len > ctx or ctx > max_ctx is counted in err_count and its rows written as zeros. */
+int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH, int32_t max_q_len,
+                                  int32_t max_ctx);
+size_t dsp_paged_mq_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
+                                    int32_t max_q_len, int32_t max_ctx, int32_t partition_tokens);
 int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                            const void* k_cache, const void* v_cache, int64_t num_slots,
                            int64_t kv_stride_slot, int64_t kv_stride_head,
                            const int32_t* block_table, int64_t bt_stride, int32_t block_size,
                            const int32_t* cu_q, const int32_t* ctx_lens, int32_t B,
                            int32_t Hq, int32_t KVH, int32_t D, float scale, int32_t max_q_len,
-                           int32_t max_ctx, void* out, int64_t o_stride_t, int64_t o_stride_h,
-                           int32_t dtype, int32_t* err_count, dsp_stream_t stream);
+                           int32_t max_ctx, int32_t partition_tokens, void* workspace,
+                           size_t workspace_bytes, void* out, int64_t o_stride_t,
+                           int64_t o_stride_h, int32_t dtype, int32_t* err_count,
+                           dsp_stream_t stream);
 
 /* ------------------------------------------------------------------------------ J5b
  * The cross-model map GEMM: C[M, N] = epilogue(A[M, K] . Bt[N, K]^T), bf16 operands,

@@ -90,3 +90,25 @@ def test_bad_lengths_are_reported_and_zeroed():
     torch.cuda.synchronize()
     assert int(err.item()) == 1
     assert torch.count_nonzero(out[:3]) == 0 and torch.count_nonzero(out[3]) > 0
+
+
+@pytest.mark.parametrize("P", [128, 256, 640, 4096])
+def test_split_k_partitions_agree(P):
+    """Key partitions merged by the LSE kernel give the same result as one pass."""
+    from dispec_amd.engine.hip_attn import paged_mq_attention
+    q_lens, ctx = [5, 5, 40, 1], [2400, 700, 1200, 3000]
+    bs, Hq, KVH, D = 16, 16, 8, 128
+    NB = sum(-(-n // bs) for n in ctx) + 3
+    tables = random_block_tables(NB, ctx, bs, 90)
+    kc, vc = randn((NB * bs, KVH, D), 91), randn((NB * bs, KVH, D), 92)
+    q = randn((sum(q_lens), Hq, D), 93)
+    bt = torch.zeros((len(ctx), max(len(t) for t in tables)), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t)
+    cu = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32)
+    out = paged_mq_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), cu.to(DEV),
+                             torch.tensor(ctx, dtype=torch.int32).to(DEV), Hq // KVH,
+                             block_size=bs, max_q_len=max(q_lens), partition_tokens=P)
+    slot_lists = [ref_cpu.context_slots(t, n, bs) for t, n in zip(tables, ctx)]
+    ref = ref_cpu.mq_attention(f64(q), f64(kc), f64(vc), slot_lists, q_lens, Hq // KVH)
+    assert_attention_close(f64(out), ref, f"P={P}")
