@@ -49,6 +49,37 @@ __device__ __forceinline__ float bf16_round(float x) {
   return __uint_as_float(uint32_t(dsp_f32_to_bf16(x)) << 16);
 }
 
+// Epilogue of four consecutive outputs (row crow, columns nb..nb+3, clipped at N) in the
+// order the reference rounds (see the header comment).
+__device__ __forceinline__ void store_c4(const f32x4& v, uint16_t* __restrict__ crow, int64_t nb,
+                                         int64_t N, const uint16_t* __restrict__ bias,
+                                         int32_t bias_mode, int32_t act, int32_t accumulate) {
+  // (the callers pass compile-time flags where they can, which prunes the branches)
+  uint16_t* dst = crow + nb;
+  const bool full = nb + 3 < N && dsp_aligned(dst, 8);
+  uint16_t ybits[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t n = nb + e;
+    if (n >= N) continue;
+    float y = v[e];
+    if (bias_mode == 1) {
+      y = bf16_round(bf16_round(y) + dsp_bf16lo(bias[n]));
+    } else if (bias_mode == 2) {
+      y = bf16_round(y + dsp_bf16lo(bias[n]));
+    } else {
+      y = bf16_round(y);
+    }
+    if (act == 1) y = bf16_round(0.5f * y * (1.f + erff(y * 0.70710678118654752f)));
+    if (accumulate) y = bf16_round(dsp_bf16lo(dst[e]) + y);
+    ybits[e] = dsp_f32_to_bf16(y);
+    if (!full) dst[e] = ybits[e];
+  }
+  if (full)
+    *reinterpret_cast<dsp_u32x2*>(dst) = dsp_u32x2{uint32_t(ybits[0]) | (uint32_t(ybits[1]) << 16),
+                                                uint32_t(ybits[2]) | (uint32_t(ybits[3]) << 16)};
+}
+
 // Load the 16-byte chunk (8 elements) of A or Bt at (row, k); zero outside the matrix.
 // kVec: `base` already points at the K tile's segment (the tile never straddles two)
 // and `k` is the column inside it.  Otherwise column k is element k % seg_len of
@@ -153,32 +184,145 @@ __global__ __launch_bounds__(kThreads) void map_gemm_kernel(
     const int64_t m = m0 + wm + 16 * i + fr;
     if (m >= M) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t nb = n0 + wn + 16 * j + 4 * (lane >> 4);
-      uint16_t* dst = c + m * ldc + nb;
-      const bool full = nb + 3 < N && dsp_aligned(dst, 8);
-      uint16_t ybits[4];
+    for (int j = 0; j < 4; ++j)
+      store_c4(acc[i][j], c + m * ldc, n0 + wn + 16 * j + 4 * (lane >> 4), N, bias, bias_mode, act,
+               accumulate);
+  }
+}
+
+// ---- large problems ---------------------------------------------------------------------
+// 256 x 256 output tile per 512-thread workgroup: 8 waves as 4 (M) x 2 (N), 64 x 128 each
+// as 4 x 8 v_mfma_f32_16x16x32 tiles.  K advances in 64-wide stages that go from global
+// memory straight into LDS (global_load_lds_dwordx4: no VGPR staging, no ds_write), two
+// stages resident (128 KiB).  A tile row is 128 bytes = 8 chunks of 16 bytes; chunk c of
+// row r is stored at slot c ^ (r & 7), so both the DMA writes (64 consecutive chunks per
+// instruction) and the MFMA fragment reads (16 rows x 4 chunks per wave) hit distinct
+// banks.  Each output still accumulates over K in 32-wide MFMA steps in increasing k, the
+// same order as map_gemm_kernel, so the two kernels give bit-identical results.
+namespace big {
+constexpr int kBM = 256, kBN = 256, kBK = 64, kWN = 2, kNW = 8, kNT = 64 * kNW;
+constexpr int kCPR = kBK / 8;                // 16-byte chunks per tile row
+constexpr int kRowB = kBK * 2;               // bytes per tile row
+constexpr int kStageB = (kBM + kBN) * kRowB;
+constexpr int kLPW = (kBM + kBN) * kCPR / 64 / kNW;  // 1-KiB DMA loads per wave per stage
+constexpr int kTM = 64, kTN = 128, kFM = kTM / 16, kFN = kTN / 16, kKS = kBK / 32;
+static_assert(kBM * kCPR % (64 * kLPW) == 0, "a wave loads rows of one operand only");
+}  // namespace big
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// The epilogue flags are template parameters: with all three variants compiled into one
+// body the epilogue's live ranges push the kernel past 256 VGPRs.
+template <int kBias, int kAct, int kAccum>
+__global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
+    const uint16_t* __restrict__ a, SegOffsets a_seg, int64_t a_seg_len, int64_t lda,
+    const uint16_t* __restrict__ bt, int64_t ldb, uint16_t* __restrict__ c, int64_t ldc,
+    int64_t M, int64_t N, int64_t K, const uint16_t* __restrict__ bias,
+    int64_t a_batch_stride, int64_t c_batch_stride) {
+  __shared__ __attribute__((aligned(1024))) char lds[2 * big::kStageB];
+  // 1-D grid over (batch, m tile, n tile), n fastest.  Workgroup ids are dealt to the 8
+  // XCDs round-robin; remap so each XCD gets a contiguous run of tiles and the n tiles
+  // sharing one A row block run on the same L2.
+  const int tn = int((N + big::kBN - 1) / big::kBN), tm = int((M + big::kBM - 1) / big::kBM);
+  int t = int(blockIdx.x);
+  const int full = int(gridDim.x) & ~7;
+  if (t < full) t = (t & 7) * (full >> 3) + (t >> 3);
+  const int bx = t % tn, by = (t / tn) % tm, bz = t / (tn * tm);
+  a += int64_t(bz) * a_batch_stride;
+  c += int64_t(bz) * c_batch_stride;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t m0 = int64_t(by) * big::kBM, n0 = int64_t(bx) * big::kBN;
+
+  // This wave's loads: instruction j covers tile rows 8 * (wave * kLPW + j) .. +7 (A rows
+  // for waves 0-3, Bt rows for waves 4-7); lane l fills slot l % 8 of row l / 8, i.e.
+  // chunk (l % 8) ^ (row & 7).  Rows past M / N are clamped to the last row (their outputs are
+  // never stored).  Element offsets fit 32 bits (checked on the host).
+  const bool loads_a = wave * big::kLPW * 64 < big::kBM * big::kCPR;
+  uint32_t off[big::kLPW];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t n = nb + e;
-        if (n >= N) continue;
-        float y = acc[i][j][e];
-        if (bias_mode == 1) {
-          y = bf16_round(bf16_round(y) + dsp_bf16lo(bias[n]));
-        } else if (bias_mode == 2) {
-          y = bf16_round(y + dsp_bf16lo(bias[n]));
-        } else {
-          y = bf16_round(y);
-        }
-        if (act == 1) y = bf16_round(0.5f * y * (1.f + erff(y * 0.70710678118654752f)));
-        if (accumulate) y = bf16_round(dsp_bf16lo(dst[e]) + y);
-        ybits[e] = dsp_f32_to_bf16(y);
-        if (!full) dst[e] = ybits[e];
-      }
-      if (full)
-        *reinterpret_cast<dsp_u32x2*>(dst) = dsp_u32x2{uint32_t(ybits[0]) | (uint32_t(ybits[1]) << 16),
-                                                    uint32_t(ybits[2]) | (uint32_t(ybits[3]) << 16)};
+  for (int j = 0; j < big::kLPW; ++j) {
+    const int r = (wave * big::kLPW + j) * (64 / big::kCPR) + lane / big::kCPR;
+    const int chunk = (lane % big::kCPR) ^ (r & 7);
+    const int64_t row = loads_a ? min<int64_t>(m0 + r, M - 1) : min<int64_t>(n0 + r - big::kBM, N - 1);
+    off[j] = uint32_t(row * (loads_a ? lda : ldb) + chunk * 8);
+  }
+  auto issue = [&](int buf, int64_t k0) {
+    // k0 is uniform, so the segment lookup is scalar; a stage never straddles segments
+    const int64_t s = k0 / a_seg_len;
+    const uint16_t* src = loads_a ? a + a_seg.get(s) + (k0 - s * a_seg_len) : bt + k0;
+    char* dst = lds + buf * big::kStageB + wave * big::kLPW * 1024;
+#pragma unroll
+    for (int j = 0; j < big::kLPW; ++j)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + off[j]),
+                                       (lds_void_t*)(dst + j * 1024), 16, 0, 0);
+  };
+
+  f32x4 acc[big::kFM][big::kFN];
+#pragma unroll
+  for (int i = 0; i < big::kFM; ++i)
+#pragma unroll
+    for (int j = 0; j < big::kFN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int wm = (wave / big::kWN) * big::kTM, wn = (wave % big::kWN) * big::kTN;
+  const int fr = lane & 15, fq = lane >> 4;
+  dsp_u32x4 fa[2][big::kFM], fb[2][big::kFN];
+  auto read_frags = [&](const char* sa, int ks, int slot) {
+    const char* sb = sa + big::kBM * big::kRowB;
+    const int chunk = ks * 4 + fq;
+#pragma unroll
+    for (int i = 0; i < big::kFM; ++i) {
+      const int r = wm + 16 * i + fr;
+      fa[slot][i] = *reinterpret_cast<const dsp_u32x4*>(sa + r * big::kRowB + ((chunk ^ (r & 7)) * 16));
     }
+#pragma unroll
+    for (int j = 0; j < big::kFN; ++j) {
+      const int r = wn + 16 * j + fr;
+      fb[slot][j] = *reinterpret_cast<const dsp_u32x4*>(sb + r * big::kRowB + ((chunk ^ (r & 7)) * 16));
+    }
+  };
+
+  const int nk = int(K / big::kBK);
+  issue(0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    // stage kt has landed for every wave, and every wave is done reading stage kt - 1,
+    // whose buffer the next DMA overwrites
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    const char* sa = lds + (kt & 1) * big::kStageB;
+    read_frags(sa, 0, 0);
+    if (kt + 1 < nk) issue((kt + 1) & 1, int64_t(kt + 1) * big::kBK);
+#pragma unroll
+    for (int ks = 0; ks < big::kKS; ++ks) {
+      if (ks + 1 < big::kKS) read_frags(sa, ks + 1, (ks + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < big::kFM; ++i)
+#pragma unroll
+        for (int j = 0; j < big::kFN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, fb[ks & 1][j]),
+                                                              __builtin_bit_cast(bf16x8, fa[ks & 1][i]),
+                                                              acc[i][j], 0, 0, 0);
+      if (ks + 1 < big::kKS) {
+        // issue the next slice's fragment reads between this slice's MFMAs
+#pragma unroll
+        for (int q = 0; q < big::kFM + big::kFN; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, big::kFM * big::kFN - (big::kFM + big::kFN), 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // acc[i][j] is a C^T tile: lane holds columns n = wn + 16j + 4*(lane/16) + e of row
+  // m = wm + 16i + lane%16.
+#pragma unroll
+  for (int i = 0; i < big::kFM; ++i) {
+    const int64_t m = m0 + wm + 16 * i + fr;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < big::kFN; ++j)
+      store_c4(acc[i][j], c + m * ldc, n0 + wn + 16 * j + 4 * fq, N, bias, kBias, kAct, kAccum);
   }
 }
 
@@ -250,14 +394,44 @@ extern "C" int dsp_kv_map_gemm(const void* a, const int64_t* a_segment_offsets,
     seg.off[i] = a_segment_offsets[i];
     vec = vec && (seg.off[i] % 8 == 0);
   }
-  const int64_t gm = (M + BM - 1) / BM, gn = (N + BN - 1) / BN;
-  DSP_HOST_CHECK(gm < (int64_t(1) << 31) && gn <= 65535, DSP_EINVAL);
-  dim3 grid(static_cast<unsigned>(gn), static_cast<unsigned>(gm), static_cast<unsigned>(batch));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* ah = static_cast<const uint16_t*>(a);
   const uint16_t* bh = static_cast<const uint16_t*>(bt);
   uint16_t* ch = static_cast<uint16_t*>(c);
   const uint16_t* biash = static_cast<const uint16_t*>(bias);
+  // Large problems (enough 256 x 256 tiles to cover the chip half a time) take the
+  // direct-to-LDS kernel; it needs 64-aligned K stages and 32-bit element offsets.
+  const int64_t big_tiles = ((M + big::kBM - 1) / big::kBM) * ((N + big::kBN - 1) / big::kBN) * batch;
+  int64_t max_a_off = 0;
+  for (int i = 0; i < num_segments; ++i) max_a_off = max(max_a_off, seg.off[i]);
+  // (bias mode 1 with gelu and accumulate -- a form no map uses -- would spill: excluded)
+  const bool use_big = vec && big_tiles >= 128 && big_tiles < (int64_t(1) << 31) &&
+                       !(bias_mode == 1 && activation == 1 && accumulate) &&
+                       K % big::kBK == 0 && segment_len % big::kBK == 0 &&
+                       max_a_off + (M - 1) * lda + segment_len <= int64_t(UINT32_MAX) &&
+                       (N - 1) * ldb + K <= int64_t(UINT32_MAX);
+  if (use_big) {
+    const unsigned grid = static_cast<unsigned>(big_tiles);
+#define DSP_BIG(B, A, C)                                                                       \
+  map_gemm_big_kernel<B, A, C><<<grid, big::kNT, 0, s>>>(ah, seg, segment_len, lda, bh, ldb, ch, \
+                                                         ldc, M, N, K, biash, a_batch_stride,  \
+                                                         c_batch_stride)
+#define DSP_BIG_B(A, C)                \
+  if (bias_mode == 0) DSP_BIG(0, A, C); \
+  else if (bias_mode == 1) DSP_BIG(1, A, C); \
+  else DSP_BIG(2, A, C)
+    if (activation == 0 && !accumulate) { DSP_BIG_B(0, 0); }
+    else if (activation == 0) { DSP_BIG_B(0, 1); }
+    else if (!accumulate) { DSP_BIG_B(1, 0); }
+    else if (bias_mode == 0) { DSP_BIG(0, 1, 1); }
+    else { DSP_BIG(2, 1, 1); }
+#undef DSP_BIG_B
+#undef DSP_BIG
+    return dsp_launch_status();
+  }
+  const int64_t gm = (M + BM - 1) / BM, gn = (N + BN - 1) / BN;
+  DSP_HOST_CHECK(gm < (int64_t(1) << 31) && gn <= 65535, DSP_EINVAL);
+  dim3 grid(static_cast<unsigned>(gn), static_cast<unsigned>(gm), static_cast<unsigned>(batch));
   if (vec)
     map_gemm_kernel<true><<<grid, kThreads, 0, s>>>(ah, seg, segment_len, lda, bh, ldb, ch, ldc, M,
                                                     N, K, biash, bias_mode, activation, accumulate,

@@ -196,3 +196,45 @@ def test_escalation_export_map_import_round_trip():
     other.import_contiguous(t2.block_ids, mk, mv)
     back = other.export_contiguous(t2.block_ids, 36)
     assert torch.equal(back[0], mk) and torch.equal(back[1], mv)
+
+
+@pytest.mark.parametrize("B,M,N,bias_mode,act,accum", [
+    (4, 2053, 1000, 1, 0, False),   # 9 x 4 x 4 = 144 tiles: ragged M and N, x @ W + b
+    (4, 2053, 1000, 2, 1, False),   # F.linear + gelu (residual down projection)
+    (4, 2053, 1000, 0, 0, True),    # no bias, accumulate (residual up projection)
+    (40, 100, 1024, 2, 1, True),    # 160 tiles of mostly clamped rows
+])
+def test_large_tile_gemm_path(B, M, N, bias_mode, act, accum):
+    """Problems of >= 128 output tiles of 256 x 256 take the direct-to-LDS kernel.  A design
+    row of two source layers (two K segments, in map order 2, 0), against the float64
+    oracle with the reference's rounding sequence, and bit-identical to the small-tile
+    kernel, which takes the first problem of the batch on its own (too few tiles)."""
+    from dispec_amd.kv.transfer import _gemm
+    g = gen(300 + M + bias_mode)
+    L, seg, layers = 3, 1024, (2, 0)
+    K = seg * len(layers)
+    src = torch.randn((B, L, M, seg), generator=g).to(torch.bfloat16)
+    bt = (torch.randn((N, K), generator=g) / 40).to(torch.bfloat16)
+    bias = torch.randn(N, generator=g).to(torch.bfloat16)
+    c0 = torch.randn((B, M, N), generator=g).to(torch.bfloat16)
+    offs = [lay * M * seg for lay in layers]
+    a_d, bt_d, bias_d = src.to(DEV), bt.to(DEV), bias.to(DEV)
+    out = c0.to(DEV)
+    _gemm(a_d, offs, seg, seg, M, bt_d, out, bias_d if bias_mode else None, bias_mode, act,
+          accum, batch=B, a_batch_stride=L * M * seg, c_batch_stride=M * N)
+    one = c0[:1].to(DEV)
+    _gemm(a_d, offs, seg, seg, M, bt_d, one, bias_d if bias_mode else None, bias_mode, act,
+          accum, batch=1, a_batch_stride=L * M * seg, c_batch_stride=M * N)
+    assert torch.equal(out[:1], one), "large- and small-tile kernels differ"
+    x = np.concatenate([src[:, lay].double().numpy() for lay in layers], axis=-1)
+    acc = x @ bt.double().numpy().T
+    rb, b = ref_cpu.round_bf16, bias.double().numpy()
+    y = rb(rb(acc) + b) if bias_mode == 1 else rb(acc + b) if bias_mode == 2 else rb(acc)
+    if act:  # the oracle's exact-erf gelu, vectorised (scipy's erf) for 8M outputs
+        from scipy.special import erf
+        yd = y.astype(np.float64)
+        y = rb(0.5 * yd * (1.0 + erf(yd / np.sqrt(2.0))))
+    if accum:
+        y = rb(c0.double().numpy() + y)
+    _assert_map_close(bits(out.cpu()), ref_cpu.f32_to_bf16(y.astype(np.float32)),
+                      f"B={B} M={M} N={N} bias={bias_mode} act={act} accum={accum}")
