@@ -398,6 +398,31 @@ def bench_c5(torch) -> dict:
     return res
 
 
+def bench_copy(torch) -> dict:
+    """A plain 1 GiB device-to-device copy (torch's copy kernel): rocprofv3 --pmc
+    FETCH_SIZE / WRITE_SIZE of this dispatch against its known 1 GiB each way gives the
+    counters' scale factor."""
+    n = 1 << 29
+    src = torch.ones(n, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    t = _time_gpu(torch, lambda: dst.copy_(src), 5)
+    return {"copy_bytes_each_way": 2 * n, "copy_GBps": 2 * 2 * n / t / 1e9}
+
+
+def _traffic_per_launch():
+    """HBM bytes per decode launch (FETCH_SIZE + WRITE_SIZE of paged_decode_kernel and
+    decode_combine_kernel, each scaled by the copy calibration), as measured by the
+    rocprofv3 passes recorded in profiles/decode_c3_traffic.md; None if absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "decode_c3_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -407,7 +432,8 @@ def main() -> int:
     ap.add_argument("--no-aux", action="store_true")
     ap.add_argument("--only", default="",
                     help="comma list of c2,c4,c5: run just these auxiliary configs and print "
-                         "their numbers (no headline line)")
+                         "their numbers (no headline line); 'copy' runs the 1 GiB plain "
+                         "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the KV data path has no cross-GPU exchange in "
@@ -419,7 +445,7 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     torch.cuda.set_device(0)
-    configs = (("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5))
+    configs = (("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5), ("copy", bench_copy))
     if args.only:
         want = set(args.only.split(","))
         aux = {}
@@ -433,7 +459,7 @@ def main() -> int:
     dec = bench_decode(torch, args.steps, args.warmup)
     aux = {}
     if not args.no_aux:
-        for name, fn in configs:
+        for name, fn in configs[:3]:
             _log(f"config {name[1:]}")
             aux.update(fn(torch))
     cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)
@@ -458,7 +484,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbps"], 1),
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(dec["achieved_gbps"] / PEAK_HBM_GBPS, 4),
-                     "traffic": None,
+                     "traffic": _traffic_per_launch(),
                      "kernel": "paged_decode_kernel + decode_combine_kernel",
                      "alg_bytes_per_launch": dec["alg_bytes"]},
         "decode_GBps": round(dec["achieved_gbps"], 1),
