@@ -28,6 +28,7 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxParts = 64;  // key partitions per tile the merge kernel accepts
+constexpr int kWinKeys = 1024; // keys per block-table window staged in LDS (8 rounds)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -58,14 +59,6 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
   return uint32_t(lo) | (uint32_t(hi) << 16);
 }
 
-// Slot of context token t of sequence b (block-table addressing), or -1 if out of range.
-__device__ __forceinline__ int64_t mq_slot(const int32_t* __restrict__ bt, int64_t bt_row,
-                                           int32_t log2_bs, int t, int64_t num_slots) {
-  const int64_t blk = bt[bt_row + (t >> log2_bs)];
-  const int64_t s = blk * (int64_t(1) << log2_bs) + (t & ((1 << log2_bs) - 1));
-  return (s >= 0 && s < num_slots) ? s : -1;
-}
-
 template <typename Tag, int D>
 __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     const uint16_t* __restrict__ q, int64_t qst, int64_t qsh, const uint16_t* __restrict__ kc,
@@ -81,10 +74,14 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   constexpr int VPL = 32 * CPR / 64; // V chunks each lane stages per 32-key step
   constexpr int PITCH = D + 8;       // LDS row pitch of the staged V chunk (elements)
 
-  __shared__ uint16_t s_v[kWaves][32][PITCH];
+  // The V slabs are dead once the key loop ends; the cross-wave merge reuses their bytes.
+  constexpr int kSlabBytes = kWaves * 32 * PITCH * 2, kAccBytes = kWaves * 16 * (D + 1) * 4;
+  __shared__ __attribute__((aligned(16))) char s_raw[kSlabBytes > kAccBytes ? kSlabBytes : kAccBytes];
   __shared__ float s_m[kWaves][16];
   __shared__ float s_l[kWaves][16];
-  __shared__ float s_acc[kWaves][16][D + 1];
+  __shared__ int32_t s_blk[kWinKeys + 1];  // block ids of the current key window
+  auto s_v = reinterpret_cast<uint16_t (*)[32][PITCH]>(s_raw);
+  auto s_acc = reinterpret_cast<float (*)[16][D + 1]>(s_raw);
 
   const int part = blockIdx.x % num_parts, tile = blockIdx.x / num_parts;
   const int kvh = blockIdx.y, b = blockIdx.z;
@@ -132,13 +129,31 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int t0 = kbeg + wave * 32; t0 < kfin; t0 += 32 * kWaves) {
+  // Rounds of 128 keys (32 per wave).  The block ids of each 1024-key window are staged
+  // in LDS first, so a key's slot costs an LDS read rather than a dependent global load.
+  const int bmask = (1 << log2_bs) - 1;
+  int win_blk = 0;  // first block of the staged window
+  auto slot_of = [&](int key) -> int64_t {
+    const int64_t sl = int64_t(s_blk[(key >> log2_bs) - win_blk]) * (bmask + 1) + (key & bmask);
+    return (sl >= 0 && sl < num_slots) ? sl : -1;
+  };
+  for (int base = kbeg; base < kfin; base += 32 * kWaves) {
+    if ((base - kbeg) % kWinKeys == 0) {
+      const int wend = min(base + kWinKeys, kfin);
+      win_blk = base >> log2_bs;
+      const int nblk = ((wend - 1) >> log2_bs) - win_blk + 1;
+      __syncthreads();  // every wave is done with the previous window
+      for (int i = threadIdx.x; i < nblk; i += kThreads) s_blk[i] = bt[bt_row + win_blk + i];
+      __syncthreads();
+    }
+    const int t0 = base + wave * 32;
+    if (t0 >= kfin) continue;
     // K operands of the two 16-key halves: lane holds key t0 + 16*st + n, dims 8*grp+32*kk.
     dsp_u32x4 kop[2][NKK];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
       const int key = t0 + 16 * st + n;
-      const int64_t s = key < kfin ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
+      const int64_t s = key < kfin ? slot_of(key) : -1;
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk)
         kop[st][kk] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(kc + s * kvs_slot + head_off +
@@ -151,7 +166,7 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     for (int i = 0; i < VPL; ++i) {
       const int idx = lane + 64 * i;
       const int key = t0 + idx / CPR;
-      const int64_t s = key < kfin ? mq_slot(bt, bt_row, log2_bs, key, num_slots) : -1;
+      const int64_t s = key < kfin ? slot_of(key) : -1;
       vst[i] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(vc + s * kvs_slot + head_off + 8 * (idx % CPR))
                       : dsp_u32x4{0u, 0u, 0u, 0u};
     }
@@ -229,6 +244,7 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   // Row sums: this lane's keys only so far; add the other three lane groups.
   lpart += dsp_shfl_xor(lpart, 16);
   lpart += dsp_shfl_xor(lpart, 32);
+  __syncthreads();  // all waves are done with the V slabs that s_acc overlays
   if (grp == 0) {
     s_m[wave][n] = m;
     s_l[wave][n] = lpart;
@@ -268,18 +284,22 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   }
 }
 
-// Merge the key partitions of one (tile, KV head, sequence): grid = (tiles, KVH, B).
-// Thread (row, dim) pairs; the partition weights 2^(m_p - M) are formed once per row in
-// LDS, then each pair streams its partial accumulators.
+// Merge the key partitions of one (tile, KV head, sequence).  Grid = (tiles * 16 / R, KVH,
+// B) with R = 256 / D rows per workgroup: one thread per (row, dim) output.  Each row's
+// partition weights 2^(m_p - M) and 1 / L are reduced across the row's first lanes and
+// kept in LDS; the partial accumulators are then read 8 partitions at a time.
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void mq_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
     int32_t G, int32_t P, int32_t num_parts, int32_t tiles_max, uint16_t* __restrict__ out,
     int64_t ost, int64_t osh) {
-  __shared__ float s_w[16][kMaxParts];
-  __shared__ float s_inv[16];
-  const int tile = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z, KVH = gridDim.y;
+  constexpr int R = 256 / D;            // rows per workgroup
+  constexpr int W = D < 64 ? D : 64;    // lanes that reduce one row's partition weights
+  __shared__ float s_w[R][kMaxParts];
+  __shared__ float s_inv[R];
+  const int tile = blockIdx.x / (16 / R), rsub = blockIdx.x % (16 / R);
+  const int kvh = blockIdx.y, b = blockIdx.z, KVH = gridDim.y;
   const int q0 = cu_q[b];
   const int qlen = cu_q[b + 1] - q0;
   const int ctx = ctx_lens[b];
@@ -291,34 +311,42 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
   const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
   if (nparts <= 1) return;  // written directly by the attention kernel
   const int64_t slot0 = ((int64_t(b) * KVH + kvh) * tiles_max + tile) * num_parts;
-  // weights: thread t handles row t / 16 and partitions t % 16, t % 16 + 16, ...
-  if (threadIdx.x < 256) {
-    const int rr = threadIdx.x >> 4, pl = threadIdx.x & 15;
+  const int rl = threadIdx.x / D, d = threadIdx.x % D;
+  const int rr = rsub * R + rl;
+  {
     float M = -INFINITY;
-    for (int p = pl; p < nparts; p += 16) M = fmaxf(M, ws_ml[2 * ((slot0 + p) * 16 + rr)]);
+    if (d < W)
+      for (int p = d; p < nparts; p += W) M = fmaxf(M, ws_ml[2 * ((slot0 + p) * 16 + rr)]);
 #pragma unroll
-    for (int mask = 1; mask < 16; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
+    for (int mask = 1; mask < W; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
     const float Mu = M == -INFINITY ? 0.f : M;
     float L = 0.f;
-    for (int p = pl; p < nparts; p += 16) {
-      const float w = dsp_exp2(ws_ml[2 * ((slot0 + p) * 16 + rr)] - Mu);
-      s_w[rr][p] = w;
-      L = fmaf(ws_ml[2 * ((slot0 + p) * 16 + rr) + 1], w, L);
-    }
+    if (d < W)
+      for (int p = d; p < nparts; p += W) {
+        const float w = dsp_exp2(ws_ml[2 * ((slot0 + p) * 16 + rr)] - Mu);
+        s_w[rl][p] = w;
+        L = fmaf(ws_ml[2 * ((slot0 + p) * 16 + rr) + 1], w, L);
+      }
 #pragma unroll
-    for (int mask = 1; mask < 16; mask <<= 1) L += dsp_shfl_xor(L, mask);
-    if (pl == 0) s_inv[rr] = L > 0.f ? 1.f / L : 0.f;
+    for (int mask = 1; mask < W; mask <<= 1) L += dsp_shfl_xor(L, mask);
+    if (d == 0) s_inv[rl] = L > 0.f ? 1.f / L : 0.f;
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 16 * D; idx += 256) {
-    const int rr = idx / D, d = idx % D;
-    const int row = r0 + rr;
-    if (row >= rows) continue;
-    float A = 0.f;
-    for (int p = 0; p < nparts; ++p) A = fmaf(ws_acc[((slot0 + p) * 16 + rr) * D + d], s_w[rr][p], A);
-    const int qrow = q0 + row / G, hh = kvh * G + row % G;
-    out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(A * s_inv[rr]);
+  const int row = r0 + rr;
+  if (row >= rows) return;
+  const float* src = ws_acc + (slot0 * 16 + rr) * D + d;
+  const int64_t pstride = int64_t(16) * D;
+  float A = 0.f;
+  for (int p0 = 0; p0 < nparts; p0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p0 + u < nparts ? src[(p0 + u) * pstride] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (p0 + u < nparts) A = fmaf(v[u], s_w[rl][p0 + u], A);
   }
+  const int qrow = q0 + row / G, hh = kvh * G + row % G;
+  out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(A * s_inv[rl]);
 }
 
 template <typename Tag, typename... A>
@@ -434,7 +462,8 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
                            ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, ws_acc, ws_ml, oh,
                            o_stride_t, o_stride_h, err_count);
   if (st != DSP_OK || num_parts <= 1) return st;
-  dim3 cgrid(static_cast<unsigned>(tiles), static_cast<unsigned>(KVH), static_cast<unsigned>(B));
+  dim3 cgrid(static_cast<unsigned>(tiles * 16 / (256 / D)), static_cast<unsigned>(KVH),
+             static_cast<unsigned>(B));
   if (dtype == DSP_BF16)
     return launch_mq_combine<Bf16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
                                       num_parts, tm, oh, o_stride_t, o_stride_h);
