@@ -485,7 +485,7 @@ def main() -> int:
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(dec["achieved_gbps"] / PEAK_HBM_GBPS, 4),
                      "traffic": _traffic_per_launch(),
-                     "kernel": "paged_decode_kernel + decode_combine_kernel",
+                     "kernel": "paged_mq_kernel (decode mode) + decode_combine_kernel",
                      "alg_bytes_per_launch": dec["alg_bytes"]},
         "decode_GBps": round(dec["achieved_gbps"], 1),
         "aux": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in aux.items()},

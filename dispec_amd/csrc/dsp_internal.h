@@ -1,0 +1,20 @@
+// Entry points shared between the library's translation units (not part of the C ABI).
+#pragma once
+
+#include "dsp_common.h"
+
+namespace dsp_detail {
+
+// Block-table decode on the multi-query MFMA kernel (paged_mq.hip) with q_len 1 per
+// sequence.  The caller (dsp_paged_decode) has validated the arguments; the kernel writes
+// partial results as ws_acc[(b * Hq + h) * num_parts + part][D] and ws_ml[...][2] (row max,
+// row sum) and the caller's combine kernel merges them.  P must be a multiple of 32.
+int mq_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
+              const uint16_t* v_cache, int64_t num_slots, int64_t kv_stride_slot,
+              int64_t kv_stride_head, const int32_t* block_table, int64_t bt_stride,
+              int32_t log2_bs, const int32_t* ctx_lens, int32_t B, int32_t KVH, int32_t G,
+              int32_t D, float scale_log2, int32_t max_ctx, int32_t P, int32_t num_parts,
+              float* ws_acc, float* ws_ml, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
+              bool f16, int32_t* err_count, hipStream_t s);
+
+}  // namespace dsp_detail

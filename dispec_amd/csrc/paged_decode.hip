@@ -20,9 +20,14 @@
 //    usual rescale at the end of the partition.
 //  * Partitions are merged by a second small kernel (log-sum-exp combine) only when a
 //    sequence spans more than one partition.
+//
+// dsp_paged_decode sends block-table calls with head_dim >= 32 to the multi-query MFMA
+// kernel of paged_mq.hip in its decode mode (measured faster on every decode shape, most
+// for GQA groups of 6+); this VALU kernel serves per-token slot tables and head_dim 16.
 #include <float.h>
 
 #include "dsp_common.h"
+#include "dsp_internal.h"
 
 namespace {
 
@@ -422,11 +427,19 @@ extern "C" int dsp_paged_decode_partition_tokens(int32_t B, int32_t KVH, int32_t
                                                  int32_t max_ctx) {
   const int step = wg_step_for(D);
   if (step == 0 || B <= 0 || KVH <= 0 || max_ctx <= 0) return step > 0 ? step : 0;
-  // Largest power-of-two multiple of the workgroup step, at most 512, that still gives
-  // the launch enough workgroups to fill 256 CUs several times over.
-  int P = step;
-  while (P * 2 <= 512) P *= 2;
-  while (P > step && int64_t(B) * KVH * ((max_ctx + P - 1) / P) < 2048) P /= 2;
+  if (D == 16) {
+    // VALU kernel: largest power-of-two multiple of the workgroup step, at most 512,
+    // that still gives the launch enough workgroups to fill 256 CUs several times over.
+    int P = step;
+    while (P * 2 <= 512) P *= 2;
+    while (P > step && int64_t(B) * KVH * ((max_ctx + P - 1) / P) < 2048) P /= 2;
+    return P;
+  }
+  // MFMA kernel (block tables, D >= 32): long partitions -- 1024 keys, halved only while
+  // the launch has fewer than 512 workgroups (measured best on 16 x 32k and 64 x 0.5-4k
+  // contexts; the slot-table kernel accepts the same sizes).
+  int P = 1024;
+  while (P > 128 && int64_t(B) * KVH * ((max_ctx + P - 1) / P) < 512) P /= 2;
   return P;
 }
 
@@ -492,7 +505,13 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   uint16_t* oh = static_cast<uint16_t*>(out);
   const bool bm = block_table != nullptr;
   int st;
-  if (dtype == DSP_BF16)
+  if (bm && D >= 32) {
+    // block tables: the MFMA kernel (its decode mode writes this function's workspace layout)
+    st = dsp_detail::mq_decode(qh, q_stride_b, q_stride_h, kh, vh, num_slots, kv_stride_slot,
+                               kv_stride_head, table, table_stride, log2_bs, ctx_lens, B, KVH, G,
+                               D, scale_log2, max_ctx, P, num_parts, ws_acc, ws_ml, oh, o_stride_b,
+                               o_stride_h, dtype == DSP_F16, err_count, s);
+  } else if (dtype == DSP_BF16)
     st = launch_decode<Bf16Tag>(D, G, bm, grid, s, qh, q_stride_b, q_stride_h, kh, vh, num_slots,
                                 kv_stride_slot, kv_stride_head, table, table_stride, log2_bs,
                                 ctx_lens, max_ctx, scale_log2, P, num_parts, ws_acc, ws_ml, oh,

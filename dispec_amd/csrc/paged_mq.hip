@@ -22,6 +22,7 @@
 #include <float.h>
 
 #include "dsp_common.h"
+#include "dsp_internal.h"
 
 namespace {
 
@@ -59,7 +60,11 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
   return uint32_t(lo) | (uint32_t(hi) << 16);
 }
 
-template <typename Tag, int D>
+// kDecode: one query per sequence (row b of q), no cu_q; the decode entry point's
+// semantics for bad lengths (a context past max_ctx is clamped and counted, an empty one
+// gives zeros) and its workspace layout ws[(b * Hq + h) * num_parts + part], which its
+// combine kernel merges.
+template <typename Tag, int D, bool kDecode>
 __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     const uint16_t* __restrict__ q, int64_t qst, int64_t qsh, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
@@ -86,14 +91,20 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   const int part = blockIdx.x % num_parts, tile = blockIdx.x / num_parts;
   const int kvh = blockIdx.y, b = blockIdx.z;
   const int KVH = gridDim.y;
-  const int q0 = cu_q[b];
-  const int qlen = cu_q[b + 1] - q0;
+  const int q0 = kDecode ? b : cu_q[b];
+  const int qlen = kDecode ? 1 : cu_q[b + 1] - q0;
   int ctx = ctx_lens[b];
   const int rows = qlen * G;
   const int r0 = tile * 16;
   if (qlen <= 0 || r0 >= rows) return;
-  const bool bad = ctx > max_ctx || ctx < qlen;
-  if (bad) {
+  bool bad = false;
+  if (kDecode) {
+    if (ctx > max_ctx || ctx < 0) {
+      if (threadIdx.x == 0 && part == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
+      ctx = ctx < 0 ? 0 : max_ctx;
+    }
+  } else if (ctx > max_ctx || ctx < qlen) {
+    bad = true;
     if (threadIdx.x == 0 && tile == 0 && part == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
     ctx = 0;  // no keys: rows are written as zeros
   }
@@ -137,6 +148,36 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     const int64_t sl = int64_t(s_blk[(key >> log2_bs) - win_blk]) * (bmask + 1) + (key & bmask);
     return (sl >= 0 && sl < num_slots) ? sl : -1;
   };
+  // K operands of the two 16-key halves of a 32-key chunk (lane: key t0 + 16*st + n, dims
+  // 8*grp + 32*kk) and the chunk's V rows to stage in LDS (zeros past kfin).
+  dsp_u32x4 kop[2][NKK], vst[VPL];
+  auto load_k = [&](int t0) {
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int key = t0 + 16 * st + n;
+      const int64_t s = key < kfin ? slot_of(key) : -1;
+#pragma unroll
+      for (int kk = 0; kk < NKK; ++kk)
+        kop[st][kk] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(kc + s * kvs_slot + head_off +
+                                                                32 * kk + 8 * grp)
+                             : dsp_u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto load_v = [&](int t0) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int idx = lane + 64 * i;
+      const int key = t0 + idx / CPR;
+      const int64_t s = key < kfin ? slot_of(key) : -1;
+      vst[i] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(vc + s * kvs_slot + head_off + 8 * (idx % CPR))
+                      : dsp_u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  // Software pipeline: once a chunk's K has fed the score MFMAs and its V sits in LDS, the
+  // same registers take the loads of this wave's chunk of the next round, which then
+  // overlap the softmax and P.V of the current one.  (Not across a window boundary: the
+  // next window's block ids are not staged yet.)
+  bool pending = false;
   for (int base = kbeg; base < kfin; base += 32 * kWaves) {
     if ((base - kbeg) % kWinKeys == 0) {
       const int wend = min(base + kWinKeys, kfin);
@@ -148,34 +189,12 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     }
     const int t0 = base + wave * 32;
     if (t0 >= kfin) continue;
-    // K operands of the two 16-key halves: lane holds key t0 + 16*st + n, dims 8*grp+32*kk.
-    dsp_u32x4 kop[2][NKK];
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      const int key = t0 + 16 * st + n;
-      const int64_t s = key < kfin ? slot_of(key) : -1;
-#pragma unroll
-      for (int kk = 0; kk < NKK; ++kk)
-        kop[st][kk] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(kc + s * kvs_slot + head_off +
-                                                                32 * kk + 8 * grp)
-                             : dsp_u32x4{0u, 0u, 0u, 0u};
+    const int tn = t0 + 32 * kWaves;
+    const bool prefetch = tn < kfin && (base + 32 * kWaves - kbeg) % kWinKeys != 0;
+    if (!pending) {
+      load_k(t0);
+      load_v(t0);
     }
-    // Stage this step's 32 V rows in the wave's LDS slab (zeros past kend).
-    dsp_u32x4 vst[VPL];
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int idx = lane + 64 * i;
-      const int key = t0 + idx / CPR;
-      const int64_t s = key < kfin ? slot_of(key) : -1;
-      vst[i] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(vc + s * kvs_slot + head_off + 8 * (idx % CPR))
-                      : dsp_u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int idx = lane + 64 * i;
-      *reinterpret_cast<dsp_u32x4*>(&s_v[wave][idx / CPR][8 * (idx % CPR)]) = vst[i];
-    }
-
     f32x4 sc[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -183,6 +202,14 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk) sc[st] = mfma32<Tag>(kop[st][kk], qop[kk], sc[st]);
     }
+    if (prefetch) load_k(tn);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int idx = lane + 64 * i;
+      *reinterpret_cast<dsp_u32x4*>(&s_v[wave][idx / CPR][8 * (idx % CPR)]) = vst[i];
+    }
+    if (prefetch) load_v(tn);
+    pending = prefetch;
     // Scale and causal mask; lane holds keys t0 + 16*st + 4*grp + j of packed row n.
     float s[2][4];
     float mx = -INFINITY;
@@ -273,6 +300,13 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     if (nparts == 1) {
       const int qrow = q0 + row / G, hh = kvh * G + row % G;
       out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(L > 0.f ? A / L : 0.f);
+    } else if (kDecode) {
+      const int64_t wrow = (int64_t(b) * KVH * G + kvh * G + row) * num_parts + part;
+      ws_acc[wrow * D + d] = A;
+      if (d == 0) {
+        ws_ml[2 * wrow] = M;
+        ws_ml[2 * wrow + 1] = L;
+      }
     } else {
       const int64_t slot = ((int64_t(b) * KVH + kvh) * tiles_max + tile) * num_parts + part;
       ws_acc[(slot * 16 + rr) * D + d] = A;
@@ -349,12 +383,12 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
   out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(A * s_inv[rl]);
 }
 
-template <typename Tag, typename... A>
+template <typename Tag, bool kDecode = false, typename... A>
 int launch_mq(int D, dim3 grid, hipStream_t s, A... args) {
   switch (D) {
-    case 32: paged_mq_kernel<Tag, 32><<<grid, kThreads, 0, s>>>(args...); break;
-    case 64: paged_mq_kernel<Tag, 64><<<grid, kThreads, 0, s>>>(args...); break;
-    case 128: paged_mq_kernel<Tag, 128><<<grid, kThreads, 0, s>>>(args...); break;
+    case 32: paged_mq_kernel<Tag, 32, kDecode><<<grid, kThreads, 0, s>>>(args...); break;
+    case 64: paged_mq_kernel<Tag, 64, kDecode><<<grid, kThreads, 0, s>>>(args...); break;
+    case 128: paged_mq_kernel<Tag, 128, kDecode><<<grid, kThreads, 0, s>>>(args...); break;
     default: return DSP_EUNSUPPORTED;
   }
   return dsp_launch_status();
@@ -373,6 +407,34 @@ int launch_mq_combine(int D, dim3 grid, hipStream_t s, A... args) {
 int64_t mq_tiles(int32_t max_q_len, int32_t G) { return (int64_t(max_q_len) * G + 15) / 16; }
 
 }  // namespace
+
+namespace dsp_detail {
+
+// Block-table decode on the MFMA kernel (q_len 1): called by dsp_paged_decode, which has
+// checked the arguments and launches its own combine over the same workspace layout.
+int mq_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const uint16_t* k_cache,
+              const uint16_t* v_cache, int64_t num_slots, int64_t kv_stride_slot,
+              int64_t kv_stride_head, const int32_t* block_table, int64_t bt_stride,
+              int32_t log2_bs, const int32_t* ctx_lens, int32_t B, int32_t KVH, int32_t G,
+              int32_t D, float scale_log2, int32_t max_ctx, int32_t P, int32_t num_parts,
+              float* ws_acc, float* ws_ml, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
+              bool f16, int32_t* err_count, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(num_parts), static_cast<unsigned>(KVH), static_cast<unsigned>(B));
+  const int32_t* no_cu = nullptr;
+  if (!f16)
+    return launch_mq<Bf16Tag, true>(D, grid, s, q, q_stride_b, q_stride_h, k_cache, v_cache,
+                                    num_slots, kv_stride_slot, kv_stride_head, block_table,
+                                    bt_stride, log2_bs, no_cu, ctx_lens, max_ctx, G, scale_log2, P,
+                                    num_parts, int32_t(1), ws_acc, ws_ml, out, o_stride_b,
+                                    o_stride_h, err_count);
+  return launch_mq<F16Tag, true>(D, grid, s, q, q_stride_b, q_stride_h, k_cache, v_cache,
+                                 num_slots, kv_stride_slot, kv_stride_head, block_table, bt_stride,
+                                 log2_bs, no_cu, ctx_lens, max_ctx, G, scale_log2, P, num_parts,
+                                 int32_t(1), ws_acc, ws_ml, out, o_stride_b, o_stride_h,
+                                 err_count);
+}
+
+}  // namespace dsp_detail
 
 extern "C" int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH,
                                              int32_t max_q_len, int32_t max_ctx) {

@@ -74,7 +74,12 @@ def test_host_argument_checks_reject_before_launch(lib):
 
 
 def test_partition_and_workspace_sizing(lib):
-    # Qwen3-4B long-context shape: 16 x 32768, KVH 8 -> 512-token partitions
-    assert lib.dsp_paged_decode_partition_tokens(16, 8, 128, 32768) == 512
+    # Qwen3-4B long-context shape: 16 x 32768, KVH 8 -> 1024-token partitions (4096 WGs)
+    assert lib.dsp_paged_decode_partition_tokens(16, 8, 128, 32768) == 1024
+    # few workgroups: halved until the launch has >= 512 (or the 128-token floor)
+    assert lib.dsp_paged_decode_partition_tokens(1, 8, 128, 32768) == 512
+    assert lib.dsp_paged_decode_partition_tokens(1, 1, 64, 1000) == 128
+    # head_dim 16 stays on the VALU kernel's sizing (power-of-two multiple of 128, <= 512)
+    assert lib.dsp_paged_decode_partition_tokens(16, 8, 16, 32768) == 512
     assert lib.dsp_paged_decode_workspace_bytes(16, 32, 128, 32768, 512) == 16 * 32 * 64 * 130 * 4
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 64, 500, 512) == 0   # one partition
