@@ -49,35 +49,68 @@ __device__ __forceinline__ float bf16_round(float x) {
   return __uint_as_float(uint32_t(dsp_f32_to_bf16(x)) << 16);
 }
 
+// Bias of the four consecutive columns nb..nb+3 (clipped at N) as floats: one 8-byte load
+// when it can, so an epilogue issues its bias loads together instead of one short load and
+// one wait per element.
+__device__ __forceinline__ void load_bias4(const uint16_t* __restrict__ bias, int64_t nb, int64_t N,
+                                           float b4[4]) {
+  if (nb + 3 < N && dsp_aligned(bias + nb, 8)) {
+    const dsp_u32x2 u = *reinterpret_cast<const dsp_u32x2*>(bias + nb);
+    b4[0] = dsp_bf16lo(u[0]);
+    b4[1] = dsp_bf16hi(u[0]);
+    b4[2] = dsp_bf16lo(u[1]);
+    b4[3] = dsp_bf16hi(u[1]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) b4[e] = nb + e < N ? dsp_bf16lo(bias[nb + e]) : 0.f;
+  }
+}
+
 // Epilogue of four consecutive outputs (row crow, columns nb..nb+3, clipped at N) in the
-// order the reference rounds (see the header comment).
+// order the reference rounds (see the header comment); b4 is their bias (bias_mode != 0).
 __device__ __forceinline__ void store_c4(const f32x4& v, uint16_t* __restrict__ crow, int64_t nb,
-                                         int64_t N, const uint16_t* __restrict__ bias,
-                                         int32_t bias_mode, int32_t act, int32_t accumulate) {
+                                         int64_t N, const float b4[4], int32_t bias_mode,
+                                         int32_t act, int32_t accumulate) {
   // (the callers pass compile-time flags where they can, which prunes the branches)
   uint16_t* dst = crow + nb;
   const bool full = nb + 3 < N && dsp_aligned(dst, 8);
+  uint16_t old[4] = {0, 0, 0, 0};
+  if (accumulate) {
+    if (full) {
+      const dsp_u32x2 u = *reinterpret_cast<const dsp_u32x2*>(dst);
+      old[0] = uint16_t(u[0]);
+      old[1] = uint16_t(u[0] >> 16);
+      old[2] = uint16_t(u[1]);
+      old[3] = uint16_t(u[1] >> 16);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (nb + e < N) old[e] = dst[e];
+    }
+  }
   uint16_t ybits[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int64_t n = nb + e;
-    if (n >= N) continue;
     float y = v[e];
     if (bias_mode == 1) {
-      y = bf16_round(bf16_round(y) + dsp_bf16lo(bias[n]));
+      y = bf16_round(bf16_round(y) + b4[e]);
     } else if (bias_mode == 2) {
-      y = bf16_round(y + dsp_bf16lo(bias[n]));
+      y = bf16_round(y + b4[e]);
     } else {
       y = bf16_round(y);
     }
     if (act == 1) y = bf16_round(0.5f * y * (1.f + erff(y * 0.70710678118654752f)));
-    if (accumulate) y = bf16_round(dsp_bf16lo(dst[e]) + y);
+    if (accumulate) y = bf16_round(dsp_bf16lo(old[e]) + y);
     ybits[e] = dsp_f32_to_bf16(y);
-    if (!full) dst[e] = ybits[e];
   }
-  if (full)
+  if (full) {
     *reinterpret_cast<dsp_u32x2*>(dst) = dsp_u32x2{uint32_t(ybits[0]) | (uint32_t(ybits[1]) << 16),
                                                 uint32_t(ybits[2]) | (uint32_t(ybits[3]) << 16)};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (nb + e < N) dst[e] = ybits[e];
+  }
 }
 
 // Load the 16-byte chunk (8 elements) of A or Bt at (row, k); zero outside the matrix.
@@ -179,14 +212,19 @@ __global__ __launch_bounds__(kThreads) void map_gemm_kernel(
 
   // acc[i][j] = C^T tile: lane holds rows n = wn + 16j + 4*(lane/16) + e, column
   // m = wm + 16i + lane%16 (the MFMA was fed Bt as its A operand).
+  float b4[4][4] = {};
+  if (bias_mode != 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) load_bias4(bias, n0 + wn + 16 * j + 4 * (lane >> 4), N, b4[j]);
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t m = m0 + wm + 16 * i + fr;
     if (m >= M) continue;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      store_c4(acc[i][j], c + m * ldc, n0 + wn + 16 * j + 4 * (lane >> 4), N, bias, bias_mode, act,
-               accumulate);
+      store_c4(acc[i][j], c + m * ldc, n0 + wn + 16 * j + 4 * (lane >> 4), N, b4[j], bias_mode,
+               act, accumulate);
   }
 }
 
@@ -316,13 +354,18 @@ __global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
 
   // acc[i][j] is a C^T tile: lane holds columns n = wn + 16j + 4*(lane/16) + e of row
   // m = wm + 16i + lane%16.
+  float b4[big::kFN][4] = {};
+  if (kBias) {
+#pragma unroll
+    for (int j = 0; j < big::kFN; ++j) load_bias4(bias, n0 + wn + 16 * j + 4 * fq, N, b4[j]);
+  }
 #pragma unroll
   for (int i = 0; i < big::kFM; ++i) {
     const int64_t m = m0 + wm + 16 * i + fr;
     if (m >= M) continue;
 #pragma unroll
     for (int j = 0; j < big::kFN; ++j)
-      store_c4(acc[i][j], c + m * ldc, n0 + wn + 16 * j + 4 * fq, N, bias, kBias, kAct, kAccum);
+      store_c4(acc[i][j], c + m * ldc, n0 + wn + 16 * j + 4 * fq, N, b4[j], kBias, kAct, kAccum);
   }
 }
 
