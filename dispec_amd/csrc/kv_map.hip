@@ -285,15 +285,23 @@ __global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
     const int64_t row = loads_a ? min<int64_t>(m0 + r, M - 1) : min<int64_t>(n0 + r - big::kBM, N - 1);
     off[j] = uint32_t(row * (loads_a ? lda : ldb) + chunk * 8);
   }
+  // Stages are issued in order; the A source (segment seg_i, column seg_k inside it) is
+  // advanced incrementally, so a segment offset is fetched once per segment boundary
+  // rather than divided out and loaded at every stage (a stage never straddles segments).
+  int64_t seg_i = 0, seg_k = 0;
+  const uint16_t* a_src = a + a_seg.off[0];
   auto issue = [&](int buf, int64_t k0) {
-    // k0 is uniform, so the segment lookup is scalar; a stage never straddles segments
-    const int64_t s = k0 / a_seg_len;
-    const uint16_t* src = loads_a ? a + a_seg.get(s) + (k0 - s * a_seg_len) : bt + k0;
+    const uint16_t* src = loads_a ? a_src + seg_k : bt + k0;
     char* dst = lds + buf * big::kStageB + wave * big::kLPW * 1024;
 #pragma unroll
     for (int j = 0; j < big::kLPW; ++j)
       __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + off[j]),
                                        (lds_void_t*)(dst + j * 1024), 16, 0, 0);
+    seg_k += big::kBK;
+    if (seg_k == a_seg_len && k0 + big::kBK < K) {
+      seg_k = 0;
+      a_src = a + a_seg.get(++seg_i);
+    }
   };
 
   f32x4 acc[big::kFM][big::kFN];
