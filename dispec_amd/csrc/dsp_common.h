@@ -63,11 +63,10 @@ __device__ __forceinline__ void dsp_st_stream(V v, V* p) { __builtin_nontemporal
 __device__ __forceinline__ float dsp_bf16lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float dsp_bf16hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
+// fp32 -> bf16, round to nearest even: one v_cvt_pk_bf16_f32 on gfx950 (NaN stays a quiet
+// NaN; finite values round exactly as the bit-twiddling form u + 0x7fff + lsb would).
 __device__ __forceinline__ uint16_t dsp_f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float dsp_f16lo(uint32_t u) {
