@@ -65,7 +65,7 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
 // gives zeros) and its workspace layout ws[(b * Hq + h) * num_parts + part], which its
 // combine kernel merges.
 template <typename Tag, int D, bool kDecode>
-__global__ __launch_bounds__(kThreads) void paged_mq_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) void paged_mq_kernel(
     const uint16_t* __restrict__ q, int64_t qst, int64_t qsh, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
     const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
@@ -76,17 +76,19 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   constexpr int NKK = D / 32;        // 32-dim K steps of the score MFMA
   constexpr int NT = D / 16;         // 16-dim output tiles
   constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
-  constexpr int VPL = 32 * CPR / 64; // V chunks each lane stages per 32-key step
-  constexpr int PITCH = D + 8;       // LDS row pitch of the staged V chunk (elements)
+  constexpr int ROWB = 2 * D;         // bytes of one K/V row
+  constexpr int SLAB = 32 * ROWB;      // one wave's staged V chunk (32 rows)
+  constexpr int VINS = SLAB / 1024;    // 1-KiB DMA loads per V chunk
+  constexpr int RPI = 1024 / ROWB;     // V rows per DMA load
 
   // The V slabs are dead once the key loop ends; the cross-wave merge reuses their bytes.
-  constexpr int kSlabBytes = kWaves * 32 * PITCH * 2, kAccBytes = kWaves * 16 * (D + 1) * 4;
-  __shared__ __attribute__((aligned(16))) char s_raw[kSlabBytes > kAccBytes ? kSlabBytes : kAccBytes];
+  constexpr int kSlabBytes = kWaves * SLAB, kAccBytes = kWaves * 16 * (D + 1) * 4;
+  __shared__ __attribute__((aligned(1024))) char s_raw[kSlabBytes > kAccBytes ? kSlabBytes : kAccBytes];
   __shared__ float s_m[kWaves][16];
   __shared__ float s_l[kWaves][16];
   __shared__ int32_t s_blk[kWinKeys + 1];  // block ids of the current key window
-  auto s_v = reinterpret_cast<uint16_t (*)[32][PITCH]>(s_raw);
   auto s_acc = reinterpret_cast<float (*)[16][D + 1]>(s_raw);
+  char* const slab_base = s_raw;
 
   const int part = blockIdx.x % num_parts, tile = blockIdx.x / num_parts;
   const int kvh = blockIdx.y, b = blockIdx.z;
@@ -149,8 +151,14 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     return (sl >= 0 && sl < num_slots) ? sl : -1;
   };
   // K operands of the two 16-key halves of a 32-key chunk (lane: key t0 + 16*st + n, dims
-  // 8*grp + 32*kk) and the chunk's V rows to stage in LDS (zeros past kfin).
-  dsp_u32x4 kop[2][NKK], vst[VPL];
+  // 8*grp + 32*kk), zeros past kfin.  The chunk's V rows go straight into the wave's LDS
+  // slab (global_load_lds_dwordx4, no registers); their 16-byte chunks are XOR-swizzled by
+  // row -- chunk c of row r at slot c ^ 2*((r >> 2) & 3) -- so that the transposed 2-byte
+  // reads of the 4 lane groups (rows 4 apart) hit different banks.  V rows past kfin
+  // repeat the last key's row: finite data whose probabilities are exactly 0.
+  dsp_u32x4 kop[2][NKK];
+  char* const slab = slab_base + wave * SLAB;
+  auto swz = [](int r, int c) { return c ^ ((2 * ((r >> 2) & 3)) & (CPR - 1)); };
   auto load_k = [&](int t0) {
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
@@ -165,12 +173,13 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
   };
   auto load_v = [&](int t0) {
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int idx = lane + 64 * i;
-      const int key = t0 + idx / CPR;
-      const int64_t s = key < kfin ? slot_of(key) : -1;
-      vst[i] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(vc + s * kvs_slot + head_off + 8 * (idx % CPR))
-                      : dsp_u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < VINS; ++i) {
+      const int row = i * RPI + lane / CPR, slot = lane % CPR;
+      const int64_t s = slot_of(min(t0 + row, kfin - 1));
+      const uint16_t* src = vc + (s >= 0 ? s : 0) * kvs_slot + head_off + 8 * swz(row, slot);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                       (__attribute__((address_space(3))) void*)(slab + i * 1024),
+                                       16, 0, 0);
     }
   };
   // Software pipeline: once a chunk's K has fed the score MFMAs and its V sits in LDS, the
@@ -192,8 +201,8 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     const int tn = t0 + 32 * kWaves;
     const bool prefetch = tn < kfin && (base + 32 * kWaves - kbeg) % kWinKeys != 0;
     if (!pending) {
-      load_k(t0);
       load_v(t0);
+      load_k(t0);
     }
     f32x4 sc[2];
 #pragma unroll
@@ -203,13 +212,6 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
       for (int kk = 0; kk < NKK; ++kk) sc[st] = mfma32<Tag>(kop[st][kk], qop[kk], sc[st]);
     }
     if (prefetch) load_k(tn);
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int idx = lane + 64 * i;
-      *reinterpret_cast<dsp_u32x4*>(&s_v[wave][idx / CPR][8 * (idx % CPR)]) = vst[i];
-    }
-    if (prefetch) load_v(tn);
-    pending = prefetch;
     // Scale and causal mask; lane holds keys t0 + 16*st + 4*grp + j of packed row n.
     float s[2][4];
     float mx = -INFINITY;
@@ -246,10 +248,16 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) acc[nt] *= alpha;
 
-    // V^T operand: lane needs dim 16*nt + n of keys {4*grp+u} (u<4) and {16+4*grp+u-4}.
+    // This chunk's V has landed in the slab: every VMEM op issued after it is the next
+    // chunk's K (2 * NKK loads, when prefetching).
+    if (prefetch)
+      __builtin_amdgcn_s_waitcnt(((2 * NKK) & 15) | 0x0F70);
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // V^T operand: lane needs dim 16*nt + n of keys {4*grp+u} (u<4) and {16+4*grp+u-4}.
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const int d = 16 * nt + n;
@@ -257,7 +265,8 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int kl = u < 4 ? 4 * grp + u : 16 + 4 * grp + (u - 4);
-        v[u] = s_v[wave][kl][d];
+        v[u] = *reinterpret_cast<const uint16_t*>(slab + kl * ROWB + 16 * swz(kl, d >> 3) +
+                                                  2 * (d & 7));
       }
       const dsp_u32x4 vop = dsp_u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]),
                                    pack2(v[6], v[7])};
@@ -266,6 +275,9 @@ __global__ __launch_bounds__(kThreads) void paged_mq_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the slab's reads are done (their values fed the MFMAs): the next chunk's V may land
+    if (prefetch) load_v(tn);
+    pending = prefetch;
   }
 
   // Row sums: this lane's keys only so far; add the other three lane groups.
