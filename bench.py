@@ -238,6 +238,54 @@ def bench_c2(torch) -> dict:
     return res
 
 
+# ------------------------------------------------------------------------------ config 1
+def bench_c1(torch) -> dict:
+    """Qwen2-0.5B shape, one layer: Hq 14, KVH 2 (G 7), D 64, a 256-block pool, contexts
+    {37, 128, 255, 511} plus the token appended this step; append + decode.  Launch-bound:
+    the times include the Python wrappers' host work between launches (0.48 MB of K/V)."""
+    from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
+    from dispec_amd.kv.paged_cache import PagedKVCache
+
+    Hq, KVH, D, bs, NB = 14, 2, 64, 16, 256
+    dev = "cuda"
+    lens = [38, 129, 256, 512]
+    gcpu = torch.Generator().manual_seed(1001)
+    perm = torch.randperm(NB, generator=gcpu).tolist()
+    tables, at = [], 0
+    for n in lens:
+        k = -(-n // bs)
+        tables.append(perm[at:at + k])
+        at += k
+    cache = PagedKVCache(1, NB, bs, KVH, D, device=dev)
+    _fill_randn(torch, cache.key, 1002)
+    _fill_randn(torch, cache.value, 1003)
+    bt = cache.block_table(tables)
+    ctx = torch.tensor(lens, dtype=torch.int32, device=dev)
+    g = torch.Generator(device=dev).manual_seed(1004)
+    q = torch.randn((len(lens), Hq, D), generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn((len(lens), KVH, D), generator=g, device=dev).to(torch.bfloat16)
+    slots = torch.tensor([t[(n - 1) // bs] * bs + (n - 1) % bs for t, n in zip(tables, lens)],
+                         device=dev)
+    out = torch.empty_like(q)
+
+    def step():
+        cache.write(0, slots, kn, kn)
+        paged_decode_attention_blocks(q, cache.key[0], cache.value[0], bt, ctx, Hq // KVH,
+                                      block_size=bs, max_ctx=max(lens), out=out)
+
+    def decode():
+        paged_decode_attention_blocks(q, cache.key[0], cache.value[0], bt, ctx, Hq // KVH,
+                                      block_size=bs, max_ctx=max(lens), out=out)
+
+    st = _time_gpu(torch, step, 50, warmup=5)
+    dec = _time_gpu(torch, decode, 50, warmup=5)
+    cache.check_errors()
+    kv_bytes = sum(lens) * KVH * D * 2 * 2
+    del cache
+    return {"c1_step_us": st * 1e6, "c1_decode_us": dec * 1e6,
+            "c1_decode_GBps": kv_bytes / dec / 1e9}
+
+
 # ------------------------------------------------------------------------------ config 4
 def bench_c4(torch) -> dict:
     """Qwen3-1.7B shape (28 L, Hq 16, KVH 8, D 128): 32 sequences share a 2050-token
@@ -431,7 +479,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-aux", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of c2,c4,c5: run just these auxiliary configs and print "
+                    help="comma list of c1,c2,c4,c5: run just these auxiliary configs and print "
                          "their numbers (no headline line); 'copy' runs the 1 GiB plain "
                          "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
@@ -445,7 +493,8 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
     torch.cuda.set_device(0)
-    configs = (("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5), ("copy", bench_copy))
+    configs = (("c1", bench_c1), ("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5),
+               ("copy", bench_copy))
     if args.only:
         want = set(args.only.split(","))
         aux = {}
@@ -459,7 +508,7 @@ def main() -> int:
     dec = bench_decode(torch, args.steps, args.warmup)
     aux = {}
     if not args.no_aux:
-        for name, fn in configs[:3]:
+        for name, fn in configs[:4]:
             _log(f"config {name[1:]}")
             aux.update(fn(torch))
     cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)
