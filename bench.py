@@ -286,6 +286,56 @@ def bench_c1(torch) -> dict:
             "c1_decode_GBps": kv_bytes / dec / 1e9}
 
 
+def bench_graph(torch) -> dict:
+    """Whole-model decode step of the reference's draft model shape (Qwen2.5-0.5B: 24
+    layers, hidden 896, Hq 14, KVH 2, D 64, vocab 151936), random-init bf16 weights:
+    eager ModelRunner.forward + logits against HipGraphDecoder replays, batch 1 and 16,
+    every sequence at 512 tokens of context.  Times are per step, host work included."""
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    from dispec_amd.engine.hip_graph import HipGraphDecoder
+    from dispec_amd.engine.model_runner import ModelRunner, SeqMeta
+    from dispec_amd.kv.paged_cache import PagedKVCache
+
+    dev, bs, ctx = "cuda", 16, 512
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=896, intermediate_size=4864,
+                      num_hidden_layers=24, num_attention_heads=14, num_key_value_heads=2,
+                      max_position_embeddings=32768, tie_word_embeddings=True)
+    torch.manual_seed(2001)
+    with torch.device(dev):
+        model = Qwen2ForCausalLM(cfg)
+    model = model.to(torch.bfloat16).eval().requires_grad_(False)
+    runner = ModelRunner(model, attn_backend="hip")
+    out = {}
+    for B in (1, 16):
+        W = ctx // bs
+        cache = PagedKVCache.for_model(cfg, B * W, bs, torch.bfloat16, dev)
+        _fill_randn(torch, cache.key, 2002)
+        _fill_randn(torch, cache.value, 2003)
+        tables = [list(range(b * W, (b + 1) * W)) for b in range(B)]
+        meta = [SeqMeta(t, 1, ctx) for t in tables]
+        toks = [7 + b for b in range(B)]
+        pos = [ctx - 1] * B
+        slots = [t[-1] * bs + bs - 1 for t in tables]
+        tt, pt, st = (torch.tensor(x, device=dev) for x in (toks, pos, slots))
+        graph = HipGraphDecoder(runner, cache, buckets=(ctx,))
+        graph.capture(batch_sizes=(B,))
+
+        def eager():
+            runner.logits(runner.forward(tt, pt, st, meta, cache))
+
+        def replay():
+            graph.decode_batch(toks, pos, slots, meta)
+
+        e = _time_gpu(torch, eager, 30, warmup=3)
+        g = _time_gpu(torch, replay, 30, warmup=3)
+        cache.check_errors()
+        out[f"graph_b{B}_eager_ms"] = e * 1e3
+        out[f"graph_b{B}_replay_ms"] = g * 1e3
+        del graph, cache
+    return out
+
+
 # ------------------------------------------------------------------------------ config 4
 def bench_c4(torch) -> dict:
     """Qwen3-1.7B shape (28 L, Hq 16, KVH 8, D 128): 32 sequences share a 2050-token
@@ -481,7 +531,8 @@ def main() -> int:
     ap.add_argument("--only", default="",
                     help="comma list of c1,c2,c4,c5: run just these auxiliary configs and print "
                          "their numbers (no headline line); 'copy' runs the 1 GiB plain "
-                         "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
+                         "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters; "
+                         "'graph' times a whole-model decode step, eager against HIP graph")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the KV data path has no cross-GPU exchange in "
@@ -494,13 +545,13 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     configs = (("c1", bench_c1), ("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5),
-               ("copy", bench_copy))
+               ("copy", bench_copy), ("graph", bench_graph))
     if args.only:
         want = set(args.only.split(","))
         aux = {}
         for name, fn in configs:
             if name in want:
-                _log(f"config {name[1:]}")
+                _log(f"config {name}")
                 aux.update(fn(torch))
         print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v)
                           for k, v in aux.items()}), flush=True)
@@ -509,7 +560,7 @@ def main() -> int:
     aux = {}
     if not args.no_aux:
         for name, fn in configs[:4]:
-            _log(f"config {name[1:]}")
+            _log(f"config {name}")
             aux.update(fn(torch))
     cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)
     line = {

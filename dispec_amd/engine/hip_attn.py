@@ -106,6 +106,16 @@ def paged_decode_attention_blocks(q, k_cache, v_cache, block_table, ctx_lens, kv
                    out=out, workspace=workspace)
 
 
+def decode_workspace(batch, num_heads, num_kv_heads, head_dim, max_ctx, device):
+    """A float32 split-K workspace big enough for every decode launch of this shape (the
+    default partition size), or None when the launch needs none.  One buffer serves all
+    layers of a forward: the launches run in stream order."""
+    L = _lib.lib()
+    P = L.dsp_paged_decode_partition_tokens(batch, num_kv_heads, head_dim, max_ctx)
+    need = L.dsp_paged_decode_workspace_bytes(batch, num_heads, head_dim, max_ctx, P)
+    return torch.empty(need // 4 + 1, dtype=torch.float32, device=device) if need else None
+
+
 def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_groups,
                        block_size=16, scale=None, max_q_len=None, max_ctx=None, out=None,
                        err=None, partition_tokens=0, workspace=None):

@@ -26,7 +26,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from dispec_amd.engine.hip_attn import paged_decode_attention_blocks, paged_mq_attention
+from dispec_amd.engine.hip_attn import (decode_workspace, paged_decode_attention_blocks,
+                                        paged_mq_attention)
 from dispec_amd.kv.paged_cache import PagedKVCache
 
 
@@ -174,9 +175,21 @@ class ModelRunner:
                 write_slots: torch.Tensor, seq_meta: list[SeqMeta],
                 cache: PagedKVCache) -> torch.Tensor:
         """Normalized hidden states (T, hidden); `logits()` projects them."""
+        return self.run_batch(token_ids, positions, write_slots, self._batch(seq_meta, cache),
+                              cache)
+
+    def run_batch(self, token_ids: torch.Tensor, positions: torch.Tensor,
+                  write_slots: torch.Tensor, batch: _Batch, cache: PagedKVCache) -> torch.Tensor:
+        """The layer loop of `forward` over batch metadata already on the device.
+
+        No host sync and, for a decode batch that brings its own workspace, no allocation
+        outside torch's allocator: this is the body a HIP graph captures."""
         cos, sin = self.rope(positions)
         x = self.embed(token_ids)
-        batch = self._batch(seq_meta, cache)
+        if batch.decode and batch.workspace is None:
+            batch.workspace = decode_workspace(
+                batch.ctx_lens.shape[0], self.num_heads, self.num_kv_heads, self.head_dim,
+                batch.max_ctx, cache.key.device)
         for i, layer in enumerate(self.layers):
             h = layer.input_layernorm(x)
             x = x + self._attention(layer, h, cos, sin, write_slots, cache, i, batch)
