@@ -5,8 +5,10 @@ long-context decode step: 36 layers, 32 query heads, 8 KV heads (GQA 4), head_di
 block_size 16, bf16, batch 16 x 32768-token contexts with random block placement.  One
 step = for each layer, append one token per sequence through the slot mapping
 (dsp_kv_append), then split-K paged decode attention over the full context
-(dsp_paged_decode, 512-token partitions, log-sum-exp combine).  `value` is decode
-attention microseconds per layer.
+(dsp_paged_decode with its automatic split: on block tables the balanced split-K, every
+wave an equal share of the keys, then the log-sum-exp combine).  `value` is decode
+attention microseconds per layer.  The same pool is also timed with the fixed 512-token
+partitions config 3 names (`c3_fixed512_*`).
 
 Reported beside it on the same JSON line:
   roofline      decode's achieved HBM GB/s = algorithmic bytes per launch (K and V of
@@ -17,7 +19,8 @@ Reported beside it on the same JSON line:
   aux           the other configurations, each timed kernel-only with device-resident
                 tables: config 2 (decode step), config 4 (copy-on-write fork, suffix
                 append, 5-query verify, evict-by-copy), config 5 (gather, map GEMM,
-                scatter) and a prefill-scale append
+                scatter), a prefill-scale append, and skewed decode batches (one
+                long context among short ones) with the balanced and the fixed split
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-aux]
 """
@@ -96,22 +99,23 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
     ctx_lens = torch.full((B,), ctx, dtype=torch.int32, device=dev)
     out = torch.empty((L, B, Hq, D), dtype=torch.bfloat16, device=dev)
     lib = _lib.lib()
-    P = lib.dsp_paged_decode_partition_tokens(B, KVH, D, ctx)
-    ws = torch.empty(lib.dsp_paged_decode_workspace_bytes(B, Hq, D, ctx, P) // 4 + 1,
-                     dtype=torch.float32, device=dev)
+    # automatic split (0): on block tables the balanced split-K, equal key shares per wave
+    P = 0
+    ws_bytes = max(lib.dsp_paged_decode_workspace_bytes(B, Hq, KVH, D, ctx, p) for p in (0, 512))
+    ws = torch.empty(ws_bytes // 4 + 1, dtype=torch.float32, device=dev)
 
-    def step(ev=None):
+    def step(ev=None, part=P):
         for layer in range(L):
             cache.write(layer, wslots, k_new[layer], v_new[layer])
             if ev is not None:
                 ev[layer][0].record()
             paged_decode_attention_blocks(q[layer], cache.key[layer], cache.value[layer], bt,
                                           ctx_lens, Hq // KVH, block_size=bs, max_ctx=ctx,
-                                          partition_tokens=P, out=out[layer], workspace=ws)
+                                          partition_tokens=part, out=out[layer], workspace=ws)
             if ev is not None:
                 ev[layer][1].record()
 
-    _log(f"config 3: warmup {warmup} steps, partition {P} tokens")
+    _log(f"config 3: warmup {warmup} steps, balanced split-K")
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -132,9 +136,21 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
     alg_bytes = B * ctx * KVH * D * 2 * 2 + 2 * B * Hq * D * 2 + B * nb_seq * 4
     avg_s = statistics.mean(decode_ms) / 1e3
     assert torch.isfinite(out).all()
+    # Config 3 as literally stated (fixed 512-token partitions + LSE combine), same pool.
+    fixed_ms = []
+    step(part=512)
+    torch.cuda.synchronize()
+    for _ in range(max(1, min(steps, 3))):
+        step(ev, part=512)
+        torch.cuda.synchronize()
+        fixed_ms.extend(e[0].elapsed_time(e[1]) for e in ev)
+    cache.check_errors()
+    fixed_s = statistics.mean(fixed_ms) / 1e3
     res = dict(us_per_layer=avg_s * 1e6, median_us_per_layer=statistics.median(decode_ms) * 1e3,
                ms_per_step=total_ms / steps, alg_bytes=alg_bytes,
-               achieved_gbps=alg_bytes / avg_s / 1e9, partition_tokens=P)
+               achieved_gbps=alg_bytes / avg_s / 1e9, split="balanced",
+               fixed512_us_per_layer=fixed_s * 1e6,
+               fixed512_GBps=alg_bytes / fixed_s / 1e9)
     del cache, q, k_new, v_new, out, ws
     torch.cuda.empty_cache()
     return res
@@ -235,6 +251,67 @@ def bench_c2(torch) -> dict:
            "c2_decode_GBps": kv_bytes / dec_s / 1e9}
     del cache
     torch.cuda.empty_cache()
+    return res
+
+
+# ------------------------------------------------------------------ skewed decode batches
+def bench_skew(torch) -> dict:
+    """Decode batches with uneven contexts (the serving case config 3's uniform batch does
+    not show), one layer, Qwen3-4B heads (Hq 32, KVH 8, D 128): 'skew' = one 32768-token
+    context beside 15 of 512; 'mixed' = 32 contexts ~U[16, 2048) with one of 16384.  Timed
+    with the automatic split (balanced: equal key shares per wave) and with fixed 1024-token
+    partitions, kernel-only, HIP events around each launch."""
+    from dispec_amd import _lib
+    from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
+
+    dev, Hq, KVH, D, bs = "cuda", 32, 8, 128, 16
+    gcpu = torch.Generator().manual_seed(4001)
+    mixed = torch.randint(16, 2048, (32,), generator=gcpu).tolist()
+    mixed[3] = 16384
+    res = {}
+    for name, ctxs in (("skew", [32768] + [512] * 15), ("mixed", mixed)):
+        B = len(ctxs)
+        need = [-(-c // bs) for c in ctxs]
+        NB = int(sum(need) * 1.25) + 8
+        kc = torch.empty((NB * bs, KVH, D), dtype=torch.bfloat16, device=dev)
+        vc = torch.empty_like(kc)
+        _fill_randn(torch, kc.view(1, -1), 4002)
+        _fill_randn(torch, vc.view(1, -1), 4003)
+        perm = torch.randperm(NB, generator=gcpu).tolist()
+        bt = torch.zeros((B, max(need)), dtype=torch.int32)
+        at = 0
+        for i, n in enumerate(need):
+            bt[i, :n] = torch.tensor(perm[at:at + n])
+            at += n
+        bt = bt.to(dev)
+        ctx = torch.tensor(ctxs, dtype=torch.int32, device=dev)
+        q = torch.randn((B, Hq, D), generator=torch.Generator(device=dev).manual_seed(4004),
+                        device=dev).to(torch.bfloat16)
+        out = torch.empty_like(q)
+        lib = _lib.lib()
+        wsb = max(lib.dsp_paged_decode_workspace_bytes(B, Hq, KVH, D, max(ctxs), p)
+                  for p in (0, 1024))
+        ws = torch.empty(wsb // 4 + 1, dtype=torch.float32, device=dev)
+        kv_bytes = sum(ctxs) * KVH * D * 2 * 2
+        for label, P in (("balanced", 0), ("fixed1024", 1024)):
+            def f():
+                paged_decode_attention_blocks(q, kc, vc, bt, ctx, Hq // KVH, block_size=bs,
+                                              max_ctx=max(ctxs), partition_tokens=P,
+                                              out=out, workspace=ws)
+            for _ in range(3):
+                f()
+            torch.cuda.synchronize()
+            ev = [_events(torch) for _ in range(20)]
+            for a, b in ev:
+                a.record()
+                f()
+                b.record()
+            torch.cuda.synchronize()
+            us = statistics.median(a.elapsed_time(b) for a, b in ev) * 1e3
+            res[f"{name}_{label}_us"] = us
+            res[f"{name}_{label}_GBps"] = kv_bytes / us / 1e3
+        del kc, vc
+        torch.cuda.empty_cache()
     return res
 
 
@@ -529,7 +606,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-aux", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of c1,c2,c4,c5: run just these auxiliary configs and print "
+                    help="comma list of c1,c2,c4,c5,skew: run just these auxiliary configs and print "
                          "their numbers (no headline line); 'copy' runs the 1 GiB plain "
                          "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters; "
                          "'graph' times a whole-model decode step, eager against HIP graph")
@@ -545,7 +622,7 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     configs = (("c1", bench_c1), ("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5),
-               ("copy", bench_copy), ("graph", bench_graph))
+               ("skew", bench_skew), ("copy", bench_copy), ("graph", bench_graph))
     if args.only:
         want = set(args.only.split(","))
         aux = {}
@@ -559,7 +636,7 @@ def main() -> int:
     dec = bench_decode(torch, args.steps, args.warmup)
     aux = {}
     if not args.no_aux:
-        for name, fn in configs[:4]:
+        for name, fn in configs[:5]:
             _log(f"config {name}")
             aux.update(fn(torch))
     cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)
@@ -579,15 +656,17 @@ def main() -> int:
         "config": {"workload": "config 3: Qwen3-4B-shape long-context decode step",
                    "layers": C3["layers"], "q_heads": C3["hq"], "kv_heads": C3["kvh"],
                    "head_dim": C3["d"], "block_size": C3["bs"], "batch": C3["batch"],
-                   "context": C3["ctx"], "partition_tokens": dec["partition_tokens"],
+                   "context": C3["ctx"], "split": dec["split"],
                    "step": "per layer: append 1 token/seq + split-K paged decode"},
         "roofline": {"bound": "hbm", "achieved": round(dec["achieved_gbps"], 1),
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                      "frac": round(dec["achieved_gbps"] / PEAK_HBM_GBPS, 4),
                      "traffic": _traffic_per_launch(),
-                     "kernel": "paged_mq_kernel (decode mode) + decode_combine_kernel",
+                     "kernel": "decode_balanced_kernel + decode_balanced_combine_kernel",
                      "alg_bytes_per_launch": dec["alg_bytes"]},
         "decode_GBps": round(dec["achieved_gbps"], 1),
+        "c3_fixed512_us_per_layer": round(dec["fixed512_us_per_layer"], 2),
+        "c3_fixed512_GBps": round(dec["fixed512_GBps"], 1),
         "aux": {k: (round(v, 3) if isinstance(v, float) else v) for k, v in aux.items()},
         "cpu_baseline": cpu,
     }

@@ -1,0 +1,571 @@
+// J3 on block tables: balanced split-K paged decode on MFMA.
+//
+// Semantics are those of dsp_paged_decode (the reference's Triton decode kernel,
+// dispec/engine/triton_attn.py:59-95): one query per sequence, query head h reads KV head
+// h / G (:70), fp32 online softmax (:86-92), output in the cache dtype (:94-95).
+//
+// Work split.  The decode work of one launch is the list of (sequence b, KV head, 16-key
+// unit) triples in sequence-major, then KV-head, then key order; a (sequence, KV head)
+// pair is a "segment".  With C units in all and W workers -- one wave each, at most as
+// many as the GPU holds at once -- worker w takes units [w*C/W, (w+1)*C/W).  Every wave
+// therefore reads the same number of K/V bytes (to one unit) whatever the spread of context
+// lengths, and all of them finish together: there is no tail of long partitions running on
+// a mostly idle GPU.  C is computed on the device from ctx_lens, so the launch needs no
+// host synchronisation and can be captured in a graph.
+//
+// A worker whose range crosses a segment boundary produces one partial result per piece
+// (row max, row sum, unnormalised accumulator).  Piece (s, w) -- segment s, worker w --
+// is stored at workspace slot s + w: along the unit list the pieces form a staircase in
+// (s, w), so s + w is unique, and the workspace holds B*KVH + W slots.  A segment inside
+// one worker's range is normalised and written to the output by that worker; the combine
+// kernel merges the pieces of every other segment.
+//
+// Per 32-key chunk a wave does what the multi-query kernel of paged_mq.hip does in its
+// decode mode: S^T = K . Q^T with the G query heads of the KV head packed into the 16 MFMA
+// columns, K straight from HBM into the A operand, V straight into a per-wave LDS slab
+// (global_load_lds_dwordx4, rows XOR-swizzled so the transposed reads are conflict-free),
+// P kept in registers as the B operand of O^T = V^T . P^T, and the next chunk's K and V
+// loads issued while the current chunk is still being consumed.  Block ids come from two
+// 64-entry windows of the block table held one entry per lane and read as scalars
+// (readlane), the second window loaded while the first is in use.
+#include <float.h>
+
+#include "dsp_common.h"
+#include "dsp_internal.h"
+#include "dsp_mfma.h"
+
+namespace {
+
+using namespace dsp_mfma;
+
+constexpr int kLog2Unit = 4;   // 16 keys per work unit
+constexpr int kOcc = 3;        // waves per SIMD the kernel is compiled for
+constexpr int kMinUnits = 4;   // a worker gets at least this many units (64 keys)
+constexpr int kMaxBatch = 512; // every wave scans ctx_lens: the balanced split stops here
+
+__device__ __forceinline__ int units_of(int ctx, int max_ctx) {
+  ctx = ctx < 0 ? 0 : (ctx > max_ctx ? max_ctx : ctx);
+  return (ctx + (1 << kLog2Unit) - 1) >> kLog2Unit;
+}
+
+__device__ __forceinline__ int clamp_ctx(int ctx, int max_ctx) {
+  return ctx < 0 ? 0 : (ctx > max_ctx ? max_ctx : ctx);
+}
+
+// Inclusive prefix sum over the 64 lanes of the wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Sum over the 64 lanes, returned as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+  return __builtin_amdgcn_readfirstlane(v);
+}
+
+// Units of one KV head summed over all sequences (the whole launch is KVH times this).
+__device__ __forceinline__ int64_t head_units(const int32_t* __restrict__ ctx_lens, int B,
+                                              int max_ctx) {
+  int64_t t = 0;
+  for (int b0 = 0; b0 < B; b0 += 64) {
+    const int b = b0 + __lane_id();
+    t += wave_sum(b < B ? units_of(ctx_lens[b], max_ctx) : 0);
+  }
+  return t;
+}
+
+// Workers that get work: at most num_workers, each with at least kMinUnits units.
+__device__ __forceinline__ int64_t active_workers(int64_t C, int num_workers) {
+  const int64_t want = (C + kMinUnits - 1) / kMinUnits;
+  return want < num_workers ? want : num_workers;
+}
+
+// block_size >= 16: a 32-key chunk starts on a multiple of 16 keys, so it touches at most
+// two blocks, whose ids are read as scalars.  kOff32: every element offset into one
+// layer's K or V cache fits in 31 bits, so addresses are a scalar base plus a 32-bit
+// per-lane byte offset.
+template <typename Tag, int D, bool kOff32>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kOcc))) void decode_balanced_kernel(
+    const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
+    const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
+    const int32_t* __restrict__ ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t max_ctx,
+    float scale_log2, int32_t num_workers, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
+    uint16_t* __restrict__ out, int64_t osb, int64_t osh, int32_t* __restrict__ err_count) {
+  constexpr int NKK = D / 32;       // 32-dim K steps of the score MFMA
+  constexpr int NT = D / 16;        // 16-dim output tiles
+  constexpr int CPR = D / 8;        // 16-byte chunks per K/V row
+  constexpr int ROWB = 2 * D;       // bytes of one K/V row
+  constexpr int SLAB = 32 * ROWB;   // one 32-key V chunk
+  constexpr int VINS = SLAB / 1024; // 1-KiB DMA loads per V chunk
+  constexpr int RPI = 1024 / ROWB;  // V rows per DMA load
+  __shared__ __attribute__((aligned(1024))) char slab[SLAB];
+
+  const int lane = threadIdx.x;
+  const int n = lane & 15;   // packed row = query head kvh*G + n (MFMA N index)
+  const int grp = lane >> 4; // lane group: K sub-range of the MFMA operands
+  const bool row_ok = n < G;
+
+  // ---- this worker's unit range and where it starts
+  const int64_t C = head_units(ctx_lens, B, max_ctx) * KVH;
+  const int64_t W = active_workers(C, num_workers);
+  const int64_t w = blockIdx.x;
+  if (w >= W) return;
+  int64_t U = w * C / W;
+  int64_t left = (w + 1) * C / W - U;
+  int b = 0, ctx = 0, nb = 0;
+  {
+    int64_t base = 0;  // per-head units of the sequences before this 64-sequence chunk
+    for (int b0 = 0; b0 < B; b0 += 64) {
+      const int bb = b0 + lane;
+      const int c = bb < B ? clamp_ctx(ctx_lens[bb], max_ctx) : 0;
+      const int v = (c + (1 << kLog2Unit) - 1) >> kLog2Unit;
+      const int incl = wave_incl_scan(v);
+      const uint64_t hit = __ballot(int64_t(KVH) * (base + incl) > U);
+      if (hit) {
+        const int f = __builtin_amdgcn_readfirstlane(
+            __ffsll(static_cast<unsigned long long>(hit)) - 1);
+        b = b0 + f;
+        ctx = __builtin_amdgcn_readlane(c, f);
+        nb = __builtin_amdgcn_readlane(v, f);
+        U -= int64_t(KVH) * (base + __builtin_amdgcn_readlane(incl, f) - nb);  // inside b
+        break;
+      }
+      base += __builtin_amdgcn_readlane(incl, 63);
+    }
+  }
+  if (nb == 0) return;  // unreachable: unit U < C lies in a non-empty sequence
+  int kvh = static_cast<int>(U / nb);
+  int u = static_cast<int>(U % nb);
+
+  const int bmask = (1 << log2_bs) - 1;
+  char* const slab_l = slab;
+  auto swz = [](int r, int c) { return c ^ ((2 * ((r >> 2) & 3)) & (CPR - 1)); };
+  bool any_bad = false;
+
+  for (;;) {
+    // ---- piece: units [u, u1) of segment (b, kvh), keys [kb, ke)
+    const int u1 = static_cast<int>(left < int64_t(nb - u) ? u + left : nb);
+    const int kb = u << kLog2Unit;
+    const int ke = min(u1 << kLog2Unit, ctx);
+    const bool whole = u == 0 && u1 == nb;
+    const int64_t bt_row = int64_t(b) * bt_stride;
+    const int64_t head_off = int64_t(kvh) * kvs_head;
+
+    dsp_u32x4 qop[NKK];
+#pragma unroll
+    for (int kk = 0; kk < NKK; ++kk)
+      qop[kk] = row_ok ? *reinterpret_cast<const dsp_u32x4*>(q + int64_t(b) * qsb +
+                                                             int64_t(kvh * G + n) * qsh + 32 * kk +
+                                                             8 * grp)
+                       : dsp_u32x4{0u, 0u, 0u, 0u};
+
+    // Block-table windows: lane i holds the id of block wblk + i (win) and wblk + 64 + i
+    // (win2).  Chunks advance by 32 keys, i.e. by at most 32 blocks, so a chunk always
+    // lies within win and win2 once the windows have been advanced for its first key.
+    int wblk = kb >> log2_bs;
+    auto load_win = [&](int first) -> int32_t {
+      const int64_t j = int64_t(first) + lane;
+      return j < bt_stride ? bt[bt_row + j] : -1;
+    };
+    int32_t win = load_win(wblk), win2 = load_win(wblk + 64);
+    auto advance = [&](int key) {
+      if ((key >> log2_bs) - wblk >= 64) {
+        wblk += 64;
+        win = win2;
+        win2 = load_win(wblk + 64);
+      }
+    };
+    // Block ids of the chunk starting at t0: its first block and the next one (scalars).
+    int32_t cb0 = 0, cb1 = 0;
+    auto chunk_blocks = [&](int t0) {
+      const int j = (t0 >> log2_bs) - wblk;  // < 64 after advance(t0); j + 1 < 128
+      cb0 = j < 64 ? __builtin_amdgcn_readlane(win, j) : __builtin_amdgcn_readlane(win2, j - 64);
+      cb1 = j + 1 < 64 ? __builtin_amdgcn_readlane(win, j + 1)
+                       : __builtin_amdgcn_readlane(win2, j + 1 - 64);
+    };
+    // Element offset of `key` of the chunk starting at t0 in one layer's cache (head
+    // included), -1 when its block id is out of range.
+    auto elem_of = [&](int t0, int key) -> int64_t {
+      const int32_t blk = ((key >> log2_bs) != (t0 >> log2_bs)) ? cb1 : cb0;
+      const int64_t sl = int64_t(blk) * (bmask + 1) + (key & bmask);
+      return (sl >= 0 && sl < num_slots) ? sl * kvs_slot + head_off : int64_t(-1);
+    };
+    auto addr = [&](const uint16_t* base, int64_t e) -> const uint16_t* {
+      if constexpr (kOff32)
+        return reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(base) +
+                                                 (static_cast<uint32_t>(e) << 1));
+      else
+        return base + e;
+    };
+
+    dsp_u32x4 kop[2][NKK];
+    // K operands of the two 16-key halves of chunk t0 (lane: key t0 + 16*st + n, dims
+    // 8*grp + 32*kk).  Keys past ke load row ke - 1 (their scores are masked to -inf
+    // below), a bad block id row 0: the loads are unconditional, so the loop head waits
+    // for exactly these loads and nothing else.
+    auto load_k = [&](int t0) {
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int key = t0 + 16 * st + n;
+        const int64_t e = elem_of(t0, min(key, ke - 1));
+        any_bad |= key < ke && e < 0;
+        const int64_t ee = e >= 0 ? e : 0;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk)
+          kop[st][kk] = *reinterpret_cast<const dsp_u32x4*>(addr(kc, ee + 32 * kk + 8 * grp));
+      }
+    };
+    // V rows of chunk t0 into the slab: chunk c of row r at slot c ^ 2*((r >> 2) & 3).
+    // Rows past ke repeat row ke - 1 (finite data, probability exactly 0).
+    auto load_v = [&](int t0) {
+#pragma unroll
+      for (int i = 0; i < VINS; ++i) {
+        const int row = i * RPI + lane / CPR, sl = lane % CPR;
+        const int64_t e = elem_of(t0, min(t0 + row, ke - 1));
+        const uint16_t* src = addr(vc, (e >= 0 ? e : 0) + 8 * swz(row, sl));
+        __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
+                                         (__attribute__((address_space(3))) void*)(slab_l + i * 1024),
+                                         16, 0, 0);
+      }
+    };
+
+    int vbase[NT < 4 ? NT : 4];  // lane's V^T read offsets for nt & 3 (see the P.V loop)
+#pragma unroll
+    for (int j = 0; j < (NT < 4 ? NT : 4); ++j)
+      vbase[j] = 4 * grp * ROWB + 32 * (j ^ (((2 * grp) & (CPR - 1)) >> 1)) + 16 * (n >> 3) +
+                 2 * (n & 7);
+
+    float m = -INFINITY, lpart = 0.f;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // K before V, as inside the loop: the loop head then waits for K only (vmcnt(VINS)),
+    // with this chunk's V still in flight, on entry and on every later iteration alike.
+    chunk_blocks(kb);
+    load_k(kb);
+    load_v(kb);
+    for (int t0 = kb; t0 < ke; t0 += 32) {
+      const int tn = t0 + 32;
+      const bool prefetch = tn < ke;
+      f32x4 sc[2];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        sc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) sc[st] = mfma32<Tag>(kop[st][kk], qop[kk], sc[st]);
+      }
+      if (prefetch) {
+        advance(tn);
+        chunk_blocks(tn);
+        load_k(tn);
+      }
+      // Scale and mask; lane holds keys t0 + 16*st + 4*grp + j of packed row n.
+      float s[2][4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = t0 + 16 * st + 4 * grp + j;
+          s[st][j] = (row_ok && key < ke) ? sc[st][j] * scale_log2 : -INFINITY;
+          mx = fmaxf(mx, s[st][j]);
+        }
+      }
+      mx = fmaxf(mx, dsp_shfl_xor(mx, 16));
+      mx = fmaxf(mx, dsp_shfl_xor(mx, 32));
+      const float m_new = fmaxf(m, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = dsp_exp2(m - m_use);
+      m = m_new;
+      float psum = 0.f;
+      uint16_t pb[8];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float p = dsp_exp2(s[st][j] - m_use);
+          psum += p;
+          pb[4 * st + j] = narrow<Tag>(p);
+        }
+      }
+      lpart = lpart * alpha + psum;
+      const dsp_u32x4 pop = dsp_u32x4{pack2(pb[0], pb[1]), pack2(pb[2], pb[3]),
+                                      pack2(pb[4], pb[5]), pack2(pb[6], pb[7])};
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) acc[nt] *= alpha;
+
+      // This chunk's V has landed once at most the next chunk's K loads (2 * NKK) and a
+      // window load remain outstanding; loads complete in issue order.
+      if (prefetch)
+        __builtin_amdgcn_s_waitcnt(((2 * NKK) & 15) | 0x0F70);
+      else
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // V^T operand: lane needs dim 16*nt + n of keys {4*grp+u} (u<4) and {16+4*grp+u-4}.
+      // Those rows all have (row >> 2) & 3 == grp, so their swizzle is one XOR with
+      // 2*grp: dim d sits at byte 32*(nt ^ y) + 16*(n >> 3) + 2*(n & 7) of the row, with
+      // y = (2*grp & (CPR-1)) / 2 < 4.  Per lane that is one base per nt & 3 plus
+      // compile-time offsets (row, nt & ~3), i.e. LDS immediates.
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        uint16_t v[8];
+#pragma unroll
+        for (int uu = 0; uu < 8; ++uu) {
+          const int krow = uu < 4 ? uu : 12 + uu;  // row minus 4*grp
+          v[uu] = *reinterpret_cast<const uint16_t*>(
+              slab_l + vbase[nt & 3] + krow * ROWB + 32 * (nt & ~3));
+        }
+        const dsp_u32x4 vop = dsp_u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]),
+                                        pack2(v[6], v[7])};
+        acc[nt] = mfma32<Tag>(vop, pop, acc[nt]);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // the slab's reads are done (their values fed the MFMAs): the next chunk's V may land
+      if (prefetch) load_v(tn);
+    }
+
+    // Row sums: this lane's keys only so far; add the other three lane groups.
+    lpart += dsp_shfl_xor(lpart, 16);
+    lpart += dsp_shfl_xor(lpart, 32);
+    if (row_ok) {
+      if (whole) {
+        const float inv = lpart > 0.f ? 1.f / lpart : 0.f;
+        uint16_t* o = out + int64_t(b) * osb + int64_t(kvh * G + n) * osh + 4 * grp;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[16 * nt + j] = narrow<Tag>(acc[nt][j] * inv);
+      } else {
+        const int64_t row = (int64_t(b) * KVH + kvh + w) * G + n;  // slot s + w, row n
+        float* a = ws_acc + row * D + 4 * grp;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<f32x4*>(a + 16 * nt) = acc[nt];
+        if (grp == 0) {
+          ws_ml[2 * row] = m;
+          ws_ml[2 * row + 1] = lpart;
+        }
+      }
+    }
+
+    left -= u1 - u;
+    if (left <= 0) break;
+    // next segment: the next KV head of b, or the first KV head of the next non-empty
+    // sequence (one exists: units remain)
+    u = 0;
+    if (++kvh == KVH) {
+      kvh = 0;
+      do {
+        if (++b >= B) break;
+        ctx = clamp_ctx(ctx_lens[b], max_ctx);
+        nb = (ctx + (1 << kLog2Unit) - 1) >> kLog2Unit;
+      } while (nb == 0);
+      if (b >= B) break;
+    }
+  }
+  if (err_count && __ballot(any_bad) && lane == 0) atomicAdd(err_count, 1);
+}
+
+// One wave per (sequence b, query head h).  Merges the pieces of segment (b, h / G) when
+// more than one worker covered it, writes zeros for an empty context, and counts a
+// context length outside [0, max_ctx] once per sequence.
+template <typename Tag, int D>
+__global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
+    const int32_t* __restrict__ ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t max_ctx,
+    int32_t num_workers, uint16_t* __restrict__ out, int64_t osb, int64_t osh,
+    int32_t* __restrict__ err_count) {
+  constexpr int NV = D > 64 ? 2 : 1;  // dims per lane: lane, lane + 64
+  __shared__ float s_w[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = blockIdx.x * 4 + wave, b = blockIdx.y;
+  if (h >= KVH * G) return;
+  int64_t total = 0, pre = 0;
+  for (int b0 = 0; b0 < B; b0 += 64) {
+    const int bb = b0 + lane;
+    const int v = bb < B ? units_of(ctx_lens[bb], max_ctx) : 0;
+    total += wave_sum(v);
+    pre += wave_sum(bb < b ? v : 0);
+  }
+  const int raw = ctx_lens[b];
+  if (h == 0 && lane == 0 && err_count && (raw < 0 || raw > max_ctx)) atomicAdd(err_count, 1);
+  const int nb = units_of(raw, max_ctx);
+  uint16_t* o = out + int64_t(b) * osb + int64_t(h) * osh;
+  const bool act = lane < D;
+  if (nb == 0) {
+    if (act) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) o[lane + 64 * j] = 0;
+    }
+    return;
+  }
+  const int64_t C = total * KVH;
+  const int64_t W = active_workers(C, num_workers);
+  const int kvh = h / G, g = h % G;
+  const int64_t cs = int64_t(KVH) * pre + int64_t(kvh) * nb, ce = cs + nb;
+  const int64_t w0 = ((cs + 1) * W - 1) / C, w1 = (ce * W - 1) / C;
+  if (w0 == w1) return;  // one worker covered the segment and wrote the output
+  const int np = static_cast<int>(w1 - w0 + 1);
+  // piece p is slot (b*KVH + kvh) + w0 + p; its row g
+  const int64_t row0 = (int64_t(b) * KVH + kvh + w0) * G + g;
+  const int64_t pstride = G;  // rows between consecutive slots
+  float M = -INFINITY;
+  for (int p = lane; p < np; p += 64) M = fmaxf(M, ws_ml[2 * (row0 + p * pstride)]);
+#pragma unroll
+  for (int mask = 1; mask < 64; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float L = 0.f, A[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) A[j] = 0.f;
+  for (int p0 = 0; p0 < np; p0 += 64) {
+    const int p = p0 + lane;
+    float wgt = 0.f;
+    if (p < np) {
+      const int64_t r = row0 + p * pstride;
+      wgt = dsp_exp2(ws_ml[2 * r] - Mu);
+      L = fmaf(ws_ml[2 * r + 1], wgt, L);
+    }
+    s_w[wave][lane] = wgt;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int cnt = min(64, np - p0);
+    const float* src = ws_acc + (row0 + int64_t(p0) * pstride) * D + (act ? lane : 0);
+    const int64_t step = pstride * D;
+    int k = 0;
+    for (; k + 8 <= cnt; k += 8) {
+      float v[8][NV];
+#pragma unroll
+      for (int uu = 0; uu < 8; ++uu)
+#pragma unroll
+        for (int j = 0; j < NV; ++j) v[uu][j] = src[int64_t(k + uu) * step + 64 * j];
+#pragma unroll
+      for (int uu = 0; uu < 8; ++uu) {
+        const float wk = s_w[wave][k + uu];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) A[j] = fmaf(v[uu][j], wk, A[j]);
+      }
+    }
+    for (; k < cnt; ++k) {
+      const float wk = s_w[wave][k];
+#pragma unroll
+      for (int j = 0; j < NV; ++j) A[j] = fmaf(src[int64_t(k) * step + 64 * j], wk, A[j]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+#pragma unroll
+  for (int mask = 1; mask < 64; mask <<= 1) L += dsp_shfl_xor(L, mask);
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  if (act) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j) o[lane + 64 * j] = narrow<Tag>(A[j] * inv);
+  }
+}
+
+template <typename Tag, int D>
+int launch_balanced_d(int W, const uint16_t* q, int64_t qsb, int64_t qsh, const uint16_t* kc,
+                      const uint16_t* vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
+                      const int32_t* bt, int64_t bt_stride, int32_t log2_bs,
+                      const int32_t* ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t max_ctx,
+                      float scale_log2, float* ws_acc, float* ws_ml, uint16_t* out, int64_t osb,
+                      int64_t osh, int32_t* err_count, hipStream_t s) {
+  // largest element offset: last slot's last head's row end
+  const bool off32 = num_slots * kvs_slot + KVH * kvs_head + D < (int64_t(1) << 31);
+  if (off32)
+    decode_balanced_kernel<Tag, D, true><<<dim3(static_cast<unsigned>(W)), 64, 0, s>>>(
+        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens, B,
+        KVH, G, max_ctx, scale_log2, W, ws_acc, ws_ml, out, osb, osh, err_count);
+  else
+    decode_balanced_kernel<Tag, D, false><<<dim3(static_cast<unsigned>(W)), 64, 0, s>>>(
+        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens, B,
+        KVH, G, max_ctx, scale_log2, W, ws_acc, ws_ml, out, osb, osh, err_count);
+  const int st = dsp_launch_status();
+  if (st != DSP_OK) return st;
+  const int Hq = KVH * G;
+  decode_balanced_combine_kernel<Tag, D><<<dim3((Hq + 3) / 4, B), 256, 0, s>>>(
+      ws_acc, ws_ml, ctx_lens, B, KVH, G, max_ctx, W, out, osb, osh, err_count);
+  return dsp_launch_status();
+}
+
+template <typename Tag, typename... A>
+int launch_balanced(int D, A... args) {
+  switch (D) {
+    case 32: return launch_balanced_d<Tag, 32>(args...);
+    case 64: return launch_balanced_d<Tag, 64>(args...);
+    case 128: return launch_balanced_d<Tag, 128>(args...);
+    default: return DSP_EUNSUPPORTED;
+  }
+}
+
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return 256;
+  return cus;
+}
+
+}  // namespace
+
+namespace dsp_detail {
+
+bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
+                             int32_t block_size) {
+  if (B < 1 || B > kMaxBatch || KVH < 1 || max_ctx < 1) return false;
+  if (block_size < (1 << kLog2Unit)) return false;
+  if (D != 32 && D != 64 && D != 128) return false;
+  // w * C stays far inside int64 for every worker index w
+  const int64_t cmax = int64_t(B) * KVH * ((int64_t(max_ctx) + 15) >> kLog2Unit);
+  return cmax < (int64_t(1) << 40);
+}
+
+int32_t balanced_workers(int32_t B, int32_t KVH, int32_t max_ctx) {
+  const int64_t cap = int64_t(device_cus()) * 4 * kOcc;
+  const int64_t cmax = int64_t(B) * KVH * ((int64_t(max_ctx) + 15) >> kLog2Unit);
+  int64_t want = (cmax + kMinUnits - 1) / kMinUnits;
+  if (want < 1) want = 1;
+  return static_cast<int32_t>(want < cap ? want : cap);
+}
+
+size_t balanced_workspace_bytes(int32_t B, int32_t KVH, int32_t G, int32_t D, int32_t max_ctx) {
+  const int64_t slots = int64_t(B) * KVH + balanced_workers(B, KVH, max_ctx);
+  return size_t(slots) * G * (size_t(D) + 2) * sizeof(float);
+}
+
+int balanced_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
+                    const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,
+                    int64_t kv_stride_slot, int64_t kv_stride_head, const int32_t* block_table,
+                    int64_t bt_stride, int32_t log2_bs, const int32_t* ctx_lens, int32_t B,
+                    int32_t KVH, int32_t G, int32_t D, float scale_log2, int32_t max_ctx,
+                    float* workspace, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
+                    bool f16, int32_t* err_count, hipStream_t s) {
+  const int32_t W = balanced_workers(B, KVH, max_ctx);
+  float* ws_acc = workspace;
+  float* ws_ml = ws_acc + (int64_t(B) * KVH + W) * G * D;
+  if (!f16)
+    return launch_balanced<Bf16Tag>(D, W, q, q_stride_b, q_stride_h, k_cache, v_cache,
+                                    num_slots, kv_stride_slot, kv_stride_head, block_table,
+                                    bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx, scale_log2,
+                                    ws_acc, ws_ml, out, o_stride_b, o_stride_h, err_count, s);
+  return launch_balanced<F16Tag>(D, W, q, q_stride_b, q_stride_h, k_cache, v_cache, num_slots,
+                                 kv_stride_slot, kv_stride_head, block_table, bt_stride, log2_bs,
+                                 ctx_lens, B, KVH, G, max_ctx, scale_log2, ws_acc, ws_ml, out,
+                                 o_stride_b, o_stride_h, err_count, s);
+}
+
+}  // namespace dsp_detail

@@ -443,12 +443,33 @@ extern "C" int dsp_paged_decode_partition_tokens(int32_t B, int32_t KVH, int32_t
   return P;
 }
 
-extern "C" size_t dsp_paged_decode_workspace_bytes(int32_t B, int32_t Hq, int32_t D,
-                                                   int32_t max_ctx, int32_t partition_tokens) {
-  if (B <= 0 || Hq <= 0 || D <= 0 || max_ctx <= 0 || partition_tokens <= 0) return 0;
-  const int64_t np = (int64_t(max_ctx) + partition_tokens - 1) / partition_tokens;
+namespace {
+
+size_t fixed_workspace_bytes(int32_t B, int32_t Hq, int32_t D, int32_t max_ctx, int32_t P) {
+  if (P <= 0) return 0;  // no kernel for this head dim: the launch is rejected anyway
+  const int64_t np = (int64_t(max_ctx) + P - 1) / P;
   if (np <= 1) return 0;
   return size_t(B) * Hq * np * (size_t(D) + 2) * sizeof(float);
+}
+
+}  // namespace
+
+extern "C" size_t dsp_paged_decode_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
+                                                   int32_t max_ctx, int32_t partition_tokens) {
+  if (B <= 0 || Hq <= 0 || KVH <= 0 || Hq % KVH != 0 || D <= 0 || max_ctx <= 0 ||
+      partition_tokens < 0)
+    return 0;
+  if (partition_tokens > 0) return fixed_workspace_bytes(B, Hq, D, max_ctx, partition_tokens);
+  // automatic: enough for whichever split the launch picks (balanced on block tables,
+  // fixed partitions on slot tables)
+  size_t need = fixed_workspace_bytes(B, Hq, D, max_ctx,
+                                      dsp_paged_decode_partition_tokens(B, KVH, D, max_ctx));
+  // (block size unknown here: size for the balanced split whenever it could apply)
+  if (dsp_detail::balanced_decode_applies(B, KVH, D, max_ctx, 16)) {
+    const size_t bal = dsp_detail::balanced_workspace_bytes(B, KVH, Hq / KVH, D, max_ctx);
+    if (bal > need) need = bal;
+  }
+  return need;
 }
 
 extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
@@ -467,6 +488,9 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   DSP_HOST_CHECK(B >= 0 && Hq > 0 && KVH > 0 && Hq % KVH == 0 && max_ctx >= 0 && num_slots >= 0,
                  DSP_EINVAL);
   DSP_HOST_CHECK(B <= 65535 && KVH <= 65535 && num_slots < (int64_t(1) << 31), DSP_EINVAL);
+  // a key whose block id is out of range reads row 0 instead: the cache must have one
+  DSP_HOST_CHECK(num_slots > 0 || B == 0 || max_ctx == 0, DSP_EINVAL);
+  DSP_HOST_CHECK(kv_stride_slot >= 0 && kv_stride_head >= 0, DSP_EINVAL);
   DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16, DSP_EUNSUPPORTED);
   const int G = Hq / KVH;
   const int step = wg_step_for(D);
@@ -487,23 +511,36 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   } else {
     DSP_HOST_CHECK(st_stride >= max_ctx, DSP_EINVAL);
   }
-  int P = partition_tokens > 0 ? partition_tokens
-                               : dsp_paged_decode_partition_tokens(B, KVH, D, max_ctx);
-  DSP_HOST_CHECK(P % step == 0 && P <= kMaxPartition, DSP_EINVAL);
-  const int num_parts = max_ctx > 0 ? (max_ctx + P - 1) / P : 1;
-  const size_t need = dsp_paged_decode_workspace_bytes(B, Hq, D, max_ctx, P);
-  DSP_HOST_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr), DSP_EWORKSPACE);
-  DSP_HOST_CHECK(need == 0 || dsp_aligned(workspace, 16), DSP_EALIGN);
-  float* ws_acc = static_cast<float*>(workspace);
-  float* ws_ml = need ? ws_acc + int64_t(B) * Hq * num_parts * D : nullptr;
+  DSP_HOST_CHECK(partition_tokens >= 0, DSP_EINVAL);
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  dim3 grid(static_cast<unsigned>(num_parts), static_cast<unsigned>(KVH), static_cast<unsigned>(B));
   const uint16_t* qh = static_cast<const uint16_t*>(q);
   const uint16_t* kh = static_cast<const uint16_t*>(k_cache);
   const uint16_t* vh = static_cast<const uint16_t*>(v_cache);
   uint16_t* oh = static_cast<uint16_t*>(out);
   const bool bm = block_table != nullptr;
+  if (bm && partition_tokens == 0 &&
+      dsp_detail::balanced_decode_applies(B, KVH, D, max_ctx, block_size)) {
+    // block tables, automatic split: every wave takes an equal share of the keys
+    const size_t need = dsp_detail::balanced_workspace_bytes(B, KVH, G, D, max_ctx);
+    DSP_HOST_CHECK(workspace_bytes >= need && workspace != nullptr, DSP_EWORKSPACE);
+    DSP_HOST_CHECK(dsp_aligned(workspace, 16), DSP_EALIGN);
+    return dsp_detail::balanced_decode(qh, q_stride_b, q_stride_h, kh, vh, num_slots,
+                                       kv_stride_slot, kv_stride_head, table, table_stride,
+                                       log2_bs, ctx_lens, B, KVH, G, D, scale_log2, max_ctx,
+                                       static_cast<float*>(workspace), oh, o_stride_b,
+                                       o_stride_h, dtype == DSP_F16, err_count, s);
+  }
+  int P = partition_tokens > 0 ? partition_tokens
+                               : dsp_paged_decode_partition_tokens(B, KVH, D, max_ctx);
+  DSP_HOST_CHECK(P % step == 0 && P <= kMaxPartition, DSP_EINVAL);
+  const int num_parts = max_ctx > 0 ? (max_ctx + P - 1) / P : 1;
+  const size_t need = fixed_workspace_bytes(B, Hq, D, max_ctx, P);
+  DSP_HOST_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr), DSP_EWORKSPACE);
+  DSP_HOST_CHECK(need == 0 || dsp_aligned(workspace, 16), DSP_EALIGN);
+  float* ws_acc = static_cast<float*>(workspace);
+  float* ws_ml = need ? ws_acc + int64_t(B) * Hq * num_parts * D : nullptr;
+  dim3 grid(static_cast<unsigned>(num_parts), static_cast<unsigned>(KVH), static_cast<unsigned>(B));
   int st;
   if (bm && D >= 32) {
     // block tables: the MFMA kernel (its decode mode writes this function's workspace layout)

@@ -23,6 +23,7 @@
 
 #include "dsp_common.h"
 #include "dsp_internal.h"
+#include "dsp_mfma.h"
 
 namespace {
 
@@ -31,34 +32,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxParts = 64;  // key partitions per tile the merge kernel accepts
 constexpr int kWinKeys = 1024; // keys per block-table window staged in LDS (8 rounds)
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-struct Bf16Tag {};
-struct F16Tag {};
-
-template <typename Tag>
-__device__ __forceinline__ f32x4 mfma32(dsp_u32x4 a, dsp_u32x4 b, f32x4 c) {
-  if constexpr (std::is_same<Tag, Bf16Tag>::value)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
-template <typename Tag>
-__device__ __forceinline__ uint16_t narrow(float f) {
-  if constexpr (std::is_same<Tag, Bf16Tag>::value)
-    return dsp_f32_to_bf16(f);
-  else
-    return dsp_f32_to_f16(f);
-}
-
-__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
-  return uint32_t(lo) | (uint32_t(hi) << 16);
-}
+using namespace dsp_mfma;
 
 // kDecode: one query per sequence (row b of q), no cu_q; the decode entry point's
 // semantics for bad lengths (a context past max_ctx is clamped and counted, an empty one

@@ -48,8 +48,8 @@ def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
         raise ValueError("out must have q's shape and dtype with head_dim contiguous")
     L = _lib.lib()
-    P = partition_tokens or L.dsp_paged_decode_partition_tokens(B, KVH, D, max_ctx)
-    need = L.dsp_paged_decode_workspace_bytes(B, Hq, D, max_ctx, P)
+    P = int(partition_tokens)  # 0: the library's automatic split
+    need = L.dsp_paged_decode_workspace_bytes(B, Hq, KVH, D, max_ctx, P)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
@@ -108,11 +108,11 @@ def paged_decode_attention_blocks(q, k_cache, v_cache, block_table, ctx_lens, kv
 
 def decode_workspace(batch, num_heads, num_kv_heads, head_dim, max_ctx, device):
     """A float32 split-K workspace big enough for every decode launch of this shape (the
-    default partition size), or None when the launch needs none.  One buffer serves all
-    layers of a forward: the launches run in stream order."""
+    automatic split), or None when the launch needs none.  One buffer serves all layers of
+    a forward: the launches run in stream order."""
     L = _lib.lib()
-    P = L.dsp_paged_decode_partition_tokens(batch, num_kv_heads, head_dim, max_ctx)
-    need = L.dsp_paged_decode_workspace_bytes(batch, num_heads, head_dim, max_ctx, P)
+    need = L.dsp_paged_decode_workspace_bytes(batch, num_heads, num_kv_heads, head_dim,
+                                              max_ctx, 0)
     return torch.empty(need // 4 + 1, dtype=torch.float32, device=device) if need else None
 
 

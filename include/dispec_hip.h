@@ -140,12 +140,22 @@ int dsp_kv_scatter(void* k_pool, void* v_pool, int64_t num_layers,
  *   k/v_cache    : one layer, [num_slots, KVH, D] with strides (kv_stride_slot,
  *                  kv_stride_head), D contiguous; same strides for K and V.
  *   ctx_lens     : int32 [B], each in [0, max_ctx].  ctx_len 0 writes zeros.
- *   partition_tokens : split-K partition length; 0 picks one from the shape.  When a
- *                  launch needs more than one partition it uses `workspace`
- *                  (dsp_paged_decode_workspace_bytes) and a second combine kernel.
- * dtype: DSP_BF16 or DSP_F16.  D in {16, 32, 64, 128}; G = Hq / KVH in 1..8. */
-size_t dsp_paged_decode_workspace_bytes(int32_t B, int32_t Hq, int32_t D, int32_t max_ctx,
-                                        int32_t partition_tokens);
+ *   partition_tokens : 0 (automatic) or a split-K partition length.
+ *                  0 with a block table, D in {32, 64, 128} and B <= 512: a balanced
+ *                  split -- the launch's (sequence, KV head, 16-key unit) work is cut into
+ *                  equal contiguous shares, one per wave, computed on the device from
+ *                  ctx_lens -- and a log-sum-exp combine kernel.  Otherwise (or with a
+ *                  slot table) fixed partitions of partition_tokens keys (0: chosen by
+ *                  dsp_paged_decode_partition_tokens) per (sequence, KV head), merged by
+ *                  the combine kernel when a sequence spans more than one.  `workspace`
+ *                  must hold dsp_paged_decode_workspace_bytes(..., partition_tokens)
+ *                  bytes (16-byte aligned) for the same arguments, on the same device.
+ * dtype: DSP_BF16 or DSP_F16.  D in {16, 32, 64, 128}; G = Hq / KVH in 1..8.
+ * err_count (optional) is incremented for a context length outside [0, max_ctx]
+ * (clamped) and, on the balanced path, once per wave that met a block id whose slots lie
+ * outside the cache (those keys are skipped). */
+size_t dsp_paged_decode_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
+                                        int32_t max_ctx, int32_t partition_tokens);
 int dsp_paged_decode_partition_tokens(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx);
 
 int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,

@@ -81,5 +81,15 @@ def test_partition_and_workspace_sizing(lib):
     assert lib.dsp_paged_decode_partition_tokens(1, 1, 64, 1000) == 128
     # head_dim 16 stays on the VALU kernel's sizing (power-of-two multiple of 128, <= 512)
     assert lib.dsp_paged_decode_partition_tokens(16, 8, 16, 32768) == 512
-    assert lib.dsp_paged_decode_workspace_bytes(16, 32, 128, 32768, 512) == 16 * 32 * 64 * 130 * 4
-    assert lib.dsp_paged_decode_workspace_bytes(4, 14, 64, 500, 512) == 0   # one partition
+    assert lib.dsp_paged_decode_workspace_bytes(16, 32, 8, 128, 32768, 512) == 16 * 32 * 64 * 130 * 4
+    assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, 512) == 0   # one partition
+    # automatic split: room for the balanced split (B*KVH + waves slots of G rows) and for
+    # the fixed partitions a slot-table launch of the same shape picks.  Without a GPU the
+    # library assumes 256 CUs: 256 * 4 SIMDs * 3 waves = 3072 waves.
+    fixed = 16 * 32 * 32 * 130 * 4                  # 1024-token partitions
+    balanced = (16 * 8 + 3072) * 4 * 130 * 4
+    assert lib.dsp_paged_decode_workspace_bytes(16, 32, 8, 128, 32768, 0) == max(fixed, balanced)
+    # a small launch: at least 4 units of 16 keys per wave -> 4*2*ceil(500/16)/4 = 64 waves
+    assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, 0) == (4 * 2 + 64) * 7 * 66 * 4
+    assert lib.dsp_paged_decode_workspace_bytes(4, 14, 3, 64, 500, 0) == 0     # 14 % 3 != 0
+    assert lib.dsp_paged_decode_workspace_bytes(1, 4, 2, 256, 64, 0) == 0      # no D=256 kernel
