@@ -13,7 +13,9 @@ partitions config 3 names (`c3_fixed512_*`).
 Reported beside it on the same JSON line:
   roofline      decode's achieved HBM GB/s = algorithmic bytes per launch (K and V of
                 every context token once, plus q, out and the block table) / average
-                launch time from HIP events on the launch stream, against 8 TB/s
+                launch time from HIP events on the launch stream, against 8 TB/s; beside
+                it two read ceilings measured in the same run (a streaming read, and the
+                decode's access pattern with no arithmetic: dsp_probe_*)
   cpu_baseline  the reference's CPU torch path (gather + repeat_interleave + SDPA) on a
                 bounded sample of the same workload, timed on this host
   aux           the other configurations, each timed kernel-only with device-resident
@@ -136,6 +138,27 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
     alg_bytes = B * ctx * KVH * D * 2 * 2 + 2 * B * Hq * D * 2 + B * nb_seq * 4
     avg_s = statistics.mean(decode_ms) / 1e3
     assert torch.isfinite(out).all()
+    # Read ceilings on this GPU, same run: a streaming read of two layers' K (2.15 GB), and
+    # the decode's access pattern (one KV head's 256-byte row slice per key, through the
+    # block table) over layer 0 with no arithmetic.
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    span = cache.key[0:2]
+
+    def stream_probe():
+        _lib.check(lib.dsp_probe_stream_read(span.data_ptr(), span.numel() * 2, 8192,
+                                             sink.data_ptr(), stream), "probe")
+
+    def slice_probe(waves):
+        _lib.check(lib.dsp_probe_slice_read(cache.key[0].data_ptr(), cache.value[0].data_ptr(),
+                                            cache.key.shape[1], bt.data_ptr(), bt.stride(0), bs,
+                                            B, KVH, ctx, waves, sink.data_ptr(), stream), "probe")
+    stream_s = _time_gpu(torch, stream_probe, 10)
+    # best of 1024, 2048 and 4096 waves
+    slice_s = min(_time_gpu(torch, lambda: slice_probe(w), 10) for w in (8, 16, 32))
+    read_ceiling = span.numel() * 2 / stream_s / 1e9
+    pattern_ceiling = B * ctx * KVH * D * 2 * 2 / slice_s / 1e9
+
     # Config 3 as literally stated (fixed 512-token partitions + LSE combine), same pool.
     fixed_ms = []
     step(part=512)
@@ -150,7 +173,8 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
                ms_per_step=total_ms / steps, alg_bytes=alg_bytes,
                achieved_gbps=alg_bytes / avg_s / 1e9, split="balanced",
                fixed512_us_per_layer=fixed_s * 1e6,
-               fixed512_GBps=alg_bytes / fixed_s / 1e9)
+               fixed512_GBps=alg_bytes / fixed_s / 1e9,
+               read_ceiling_GBps=read_ceiling, pattern_ceiling_GBps=pattern_ceiling)
     del cache, q, k_new, v_new, out, ws
     torch.cuda.empty_cache()
     return res
@@ -663,7 +687,9 @@ def main() -> int:
                      "frac": round(dec["achieved_gbps"] / PEAK_HBM_GBPS, 4),
                      "traffic": _traffic_per_launch(),
                      "kernel": "decode_balanced_kernel + decode_balanced_combine_kernel",
-                     "alg_bytes_per_launch": dec["alg_bytes"]},
+                     "alg_bytes_per_launch": dec["alg_bytes"],
+                     "measured_read_ceiling_GBps": round(dec["read_ceiling_GBps"], 1),
+                     "measured_decode_pattern_ceiling_GBps": round(dec["pattern_ceiling_GBps"], 1)},
         "decode_GBps": round(dec["achieved_gbps"], 1),
         "c3_fixed512_us_per_layer": round(dec["fixed512_us_per_layer"], 2),
         "c3_fixed512_GBps": round(dec["fixed512_GBps"], 1),

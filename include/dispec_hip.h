@@ -240,6 +240,24 @@ int dsp_kv_rope(const void* x, int64_t x_layer_stride, void* y, int64_t y_layer_
                 const float* sin_table, int32_t direction, int32_t in_dtype, int32_t out_dtype,
                 dsp_stream_t stream);
 
+/* ------------------------------------------------------------------ roofline probes
+ * Measurement helpers with no counterpart in the reference: read-only kernels that
+ * calibrate the decode kernels' achieved bandwidth (bench.py reports them beside the
+ * roofline).
+ *   dsp_probe_stream_read: `workgroups` workgroups stream `bytes` of `buf` (16-byte
+ *     aligned) once.
+ *   dsp_probe_slice_read: the paged decode's access pattern without its arithmetic --
+ *     for each (sequence, KV head) `waves_per_seq_head` waves read that head's 128-dim
+ *     bf16 row of K and V for all `ctx` keys through `block_table`; caches are
+ *     [num_slots, KVH, 128] contiguous; ctx a multiple of 32 * waves_per_seq_head.
+ * Both store one word to `sink` only if what they read hashes to a sentinel. */
+int dsp_probe_stream_read(const void* buf, int64_t bytes, int32_t workgroups, uint32_t* sink,
+                          dsp_stream_t stream);
+int dsp_probe_slice_read(const void* k_cache, const void* v_cache, int64_t num_slots,
+                         const int32_t* block_table, int64_t bt_stride, int32_t block_size,
+                         int32_t B, int32_t KVH, int32_t ctx, int32_t waves_per_seq_head,
+                         uint32_t* sink, dsp_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

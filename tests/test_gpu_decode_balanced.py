@@ -90,6 +90,34 @@ def test_all_groups_and_head_dims(hip, D, G):
     assert_attention_close(f64(out), ref, f"D={D} G={G}")
 
 
+@pytest.mark.parametrize("KVH,G", [(1, 8), (3, 2), (5, 3)])
+def test_odd_kv_heads(hip, KVH, G):
+    """Odd KV-head counts (MQA, KVH 3 and 5): segments of every head of a sequence."""
+    lens = [900, 33, 0, 2000, 16]
+    out, ref = _run(lens, KVH, G, 128, 16, 1450 + KVH)
+    assert_attention_close(f64(out), ref, f"KVH={KVH} G={G}")
+
+
+def test_strided_heads(hip):
+    """Heads not adjacent in memory (a head stride larger than head_dim, slot stride larger
+    than KVH * head_dim)."""
+    from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
+    KVH, G, D, bs = 4, 2, 64, 16
+    lens = [100, 300]
+    NB = sum(-(-n // bs) for n in lens) + 2
+    tables = random_block_tables(NB, lens, bs, 1460)
+    big_k = randn((NB * bs, KVH, 2 * D), 1461)
+    big_v = randn((NB * bs, KVH, 2 * D), 1462)
+    kc, vc = big_k[:, :, :D], big_v[:, :, :D]            # head stride 2*D, slot stride 2*KVH*D
+    q = randn((2, KVH * G, D), 1463)
+    out = paged_decode_attention_blocks(q.to(DEV), big_k.to(DEV)[:, :, :D],
+                                        big_v.to(DEV)[:, :, :D], _bt(tables).to(DEV),
+                                        torch.tensor(lens, dtype=torch.int32).to(DEV), G)
+    ref = ref_cpu.decode_attention(f64(q), f64(kc), f64(vc), _slot_table(tables, lens, bs),
+                                   lens, G)
+    assert_attention_close(f64(out), ref, "strided heads")
+
+
 def test_fp16(hip):
     lens = [700, 33, 2048, 1]
     out, ref = _run(lens, 4, 2, 128, 16, 1500, dtype=torch.float16)
