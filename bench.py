@@ -21,8 +21,9 @@ Reported beside it on the same JSON line:
   aux           the other configurations, each timed kernel-only with device-resident
                 tables: config 2 (decode step), config 4 (copy-on-write fork, suffix
                 append, 5-query verify, evict-by-copy), config 5 (gather, map GEMM,
-                scatter), a prefill-scale append, and skewed decode batches (one
-                long context among short ones) with the balanced and the fixed split
+                scatter), a prefill-scale append, skewed decode batches (one long
+                context among short ones) with the balanced and the fixed split, and the
+                measured streaming-copy ceiling the byte-moving kernels are bounded by
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-aux]
 """
@@ -608,6 +609,29 @@ def bench_copy(torch) -> dict:
     return {"copy_bytes_each_way": 2 * n, "copy_GBps": 2 * 2 * n / t / 1e9}
 
 
+def bench_copy_ceiling(torch) -> dict:
+    """The ceiling of the byte-moving kernels on this GPU: a 2 GiB streaming copy
+    (dsp_probe_stream_copy, non-temporal loads and stores), best of three grid sizes,
+    read + write bytes over time."""
+    from dispec_amd import _lib
+    lib = _lib.lib()
+    n = 2 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    src.fill_(7)
+    stream = torch.cuda.current_stream().cuda_stream
+    best = None
+    for wgs in (2048, 8192, 32768):
+        def f():
+            _lib.check(lib.dsp_probe_stream_copy(src.data_ptr(), dst.data_ptr(), n, wgs, stream),
+                       "probe")
+        t = _time_gpu(torch, f, 10)
+        best = t if best is None else min(best, t)
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"copy_ceiling_GBps": 2 * n / best / 1e9}
+
+
 def _traffic_per_launch():
     """HBM bytes per decode launch (FETCH_SIZE + WRITE_SIZE of paged_decode_kernel and
     decode_combine_kernel, each scaled by the copy calibration), as measured by the
@@ -630,7 +654,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-aux", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of c1,c2,c4,c5,skew: run just these auxiliary configs and print "
+                    help="comma list of c1,c2,c4,c5,skew,ceiling: run just these auxiliary configs and print "
                          "their numbers (no headline line); 'copy' runs the 1 GiB plain "
                          "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters; "
                          "'graph' times a whole-model decode step, eager against HIP graph")
@@ -646,7 +670,8 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     configs = (("c1", bench_c1), ("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5),
-               ("skew", bench_skew), ("copy", bench_copy), ("graph", bench_graph))
+               ("skew", bench_skew), ("ceiling", bench_copy_ceiling), ("copy", bench_copy),
+               ("graph", bench_graph))
     if args.only:
         want = set(args.only.split(","))
         aux = {}
@@ -660,7 +685,7 @@ def main() -> int:
     dec = bench_decode(torch, args.steps, args.warmup)
     aux = {}
     if not args.no_aux:
-        for name, fn in configs[:5]:
+        for name, fn in configs[:6]:
             _log(f"config {name}")
             aux.update(fn(torch))
     cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)

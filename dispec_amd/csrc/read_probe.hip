@@ -1,5 +1,6 @@
-// Read-bandwidth probes for the roofline: what this GPU's HBM delivers to (1) a plain
-// streaming read and (2) a read with the paged decode's access pattern, with no compute.
+// Bandwidth probes for the roofline: what this GPU's HBM delivers to (1) a plain streaming
+// read, (2) a read with the paged decode's access pattern, with no compute, and (3) a plain
+// streaming copy (the ceiling of the append / gather / scatter / block-copy kernels).
 // They calibrate the decode kernel's measured GB/s: the datasheet peak (8 TB/s) is not
 // reachable by any read, and the slot-major pool layout (one KV head's 256-byte slice of
 // every 2 KiB slot row) caps what the decode can fetch below a streaming read.  Both probes
@@ -68,7 +69,41 @@ __global__ __launch_bounds__(64) void slice_read_kernel(const uint16_t* __restri
   if (r == 0x9e3779b9u) sink[0] = r;
 }
 
+// Streaming copy: each workgroup copies a contiguous span, 4 loads of 16 bytes per lane in
+// flight, then their stores (non-temporal both ways).
+__global__ __launch_bounds__(256) void stream_copy_kernel(const dsp_u32x4* __restrict__ src,
+                                                          dsp_u32x4* __restrict__ dst,
+                                                          int64_t n16, int64_t per_wg) {
+  const int64_t base = int64_t(blockIdx.x) * per_wg;
+  const int64_t end = base + per_wg < n16 ? base + per_wg : n16;
+  for (int64_t i = base + threadIdx.x; i < end; i += 256 * 4) {
+    dsp_u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t j = i + u * 256;
+      if (j < end) v[u] = dsp_ld_stream(src + j);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t j = i + u * 256;
+      if (j < end) dsp_st_stream(v[u], dst + j);
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int dsp_probe_stream_copy(const void* src, void* dst, int64_t bytes,
+                                     int32_t workgroups, dsp_stream_t stream) {
+  DSP_HOST_CHECK(src && dst && bytes >= 16 && workgroups > 0, DSP_EINVAL);
+  DSP_HOST_CHECK(dsp_aligned(src, 16) && dsp_aligned(dst, 16), DSP_EALIGN);
+  const int64_t n16 = bytes / 16;
+  const int64_t per = (n16 + workgroups - 1) / workgroups;
+  stream_copy_kernel<<<dim3(static_cast<unsigned>(workgroups)), 256, 0,
+                       static_cast<hipStream_t>(stream)>>>(
+      static_cast<const dsp_u32x4*>(src), static_cast<dsp_u32x4*>(dst), n16, per);
+  return dsp_launch_status();
+}
 
 extern "C" int dsp_probe_stream_read(const void* buf, int64_t bytes, int32_t workgroups,
                                      uint32_t* sink, dsp_stream_t stream) {

@@ -241,9 +241,9 @@ int dsp_kv_rope(const void* x, int64_t x_layer_stride, void* y, int64_t y_layer_
                 dsp_stream_t stream);
 
 /* ------------------------------------------------------------------ roofline probes
- * Measurement helpers with no counterpart in the reference: read-only kernels that
- * calibrate the decode kernels' achieved bandwidth (bench.py reports them beside the
- * roofline).
+ * Measurement helpers with no counterpart in the reference: kernels that calibrate the
+ * achieved bandwidth of the decode and byte-moving kernels (bench.py reports them beside
+ * the roofline).
  *   dsp_probe_stream_read: `workgroups` workgroups stream `bytes` of `buf` (16-byte
  *     aligned) once.
  *   dsp_probe_slice_read: the paged decode's access pattern without its arithmetic --
@@ -252,6 +252,10 @@ int dsp_kv_rope(const void* x, int64_t x_layer_stride, void* y, int64_t y_layer_
  *     [num_slots, KVH, 128] contiguous; ctx a multiple of 32 * waves_per_seq_head.
  * Both store one word to `sink` only if what they read hashes to a sentinel. */
 int dsp_probe_stream_read(const void* buf, int64_t bytes, int32_t workgroups, uint32_t* sink,
+                          dsp_stream_t stream);
+/*   dsp_probe_stream_copy: `workgroups` workgroups copy `bytes` from src to dst (both
+ *     16-byte aligned, not overlapping) once: the ceiling of the byte-moving kernels. */
+int dsp_probe_stream_copy(const void* src, void* dst, int64_t bytes, int32_t workgroups,
                           dsp_stream_t stream);
 int dsp_probe_slice_read(const void* k_cache, const void* v_cache, int64_t num_slots,
                          const int32_t* block_table, int64_t bt_stride, int32_t block_size,
