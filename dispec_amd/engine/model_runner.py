@@ -6,7 +6,8 @@ RMSNorms, q/k/v/o projections (optionally fused, :93-118), SwiGLU MLP, lm_head -
 the HF modules, unchanged.  What the backend replaces is the KV path inside `_attention`
 (:127-185) and the per-forward batch build in `forward` (:189-212):
 
-  * cache.write                      -> dsp_kv_append (K and V in one launch)
+  * q_norm / k_norm, RoPE on q and k,  -> dsp_qk_norm_rope_append (one launch; the torch
+    cache.write (:142-148)               ops' rounding points)
   * all-decode batch (every q_len 1)  -> dsp_paged_decode, split-K over a device block
                                         table built once per forward (one H2D copy, no
                                         per-token slot table and no per-sequence loop)
@@ -28,6 +29,7 @@ import torch.nn.functional as F
 
 from dispec_amd.engine.hip_attn import (decode_workspace, paged_decode_attention_blocks,
                                         paged_mq_attention)
+from dispec_amd.engine.hip_prologue import qk_norm_rope_append
 from dispec_amd.kv.paged_cache import PagedKVCache
 
 
@@ -38,15 +40,6 @@ class SeqMeta:
     block_ids: list[int]
     q_len: int      # new (query) tokens this step
     ctx_len: int    # context length including the new tokens
-
-
-def _rotate_half(x: torch.Tensor) -> torch.Tensor:
-    x1, x2 = x.chunk(2, dim=-1)
-    return torch.cat((-x2, x1), dim=-1)
-
-
-def _apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    return x * cos.unsqueeze(1) + _rotate_half(x) * sin.unsqueeze(1)
 
 
 @dataclass
@@ -151,13 +144,10 @@ class ModelRunner:
             q = attn.q_proj(x).view(T, self.num_heads, self.head_dim)
             k = attn.k_proj(x).view(T, self.num_kv_heads, self.head_dim)
             v = attn.v_proj(x).view(T, self.num_kv_heads, self.head_dim)
-        if self.qk_norm:
-            q = attn.q_norm(q)
-            k = attn.k_norm(k)
-        q = _apply_rope(q, cos, sin)
-        k = _apply_rope(k, cos, sin)
-
-        cache.write(layer_idx, write_slots, k, v)
+        # q_norm / k_norm (Qwen3), RoPE on q and k, and cache.write(k, v): one launch
+        q = qk_norm_rope_append(q, k, v, cos, sin, write_slots, cache, layer_idx,
+                                attn.q_norm if self.qk_norm else None,
+                                attn.k_norm if self.qk_norm else None)
         if batch.decode:
             o = paged_decode_attention_blocks(
                 q, cache.key[layer_idx], cache.value[layer_idx], batch.block_table,

@@ -240,6 +240,36 @@ int dsp_kv_rope(const void* x, int64_t x_layer_stride, void* y, int64_t y_layer_
                 const float* sin_table, int32_t direction, int32_t in_dtype, int32_t out_dtype,
                 dsp_stream_t stream);
 
+/* ------------------------------------------------------------------------------ J1+
+ * The attention prologue of one layer in one launch: per-head RMSNorm of q and k
+ * (optional), RoPE on q and k, and the append of k and v into the paged pool.
+ * Replaces ModelRunner._attention's op sequence (dispec/engine/model_runner.py:142-148):
+ *     q = q_norm(q); k = k_norm(k)          Qwen3RMSNorm: var = mean(x^2) in fp32,
+ *                                          y = w * dtype(x * rsqrt(var + eps))
+ *     q = q * cos + rotate_half(q) * sin   (:49-50 there), each product and the sum
+ *     k = k * cos + rotate_half(k) * sin    rounded to the dtype, as torch does
+ *     cache.write(layer, slots, k, v)      (paged_cache.py:61-68)
+ *   q, k, v      : [T, Hq | KVH, D] with (token, head) strides; D contiguous.
+ *   q/k_norm_weight : [D] RMSNorm weights, both or neither (NULL: no norm, Qwen2).
+ *   cos/sin_table: [T, D] in the model dtype (the model's rotary tables), row stride.
+ *   slots        : int64 [T] pool slots of the new tokens (out of range: counted in
+ *                  err_count, that token's k/v not written).
+ *   q_out        : [T, Hq, D] rotated q (may alias q when the strides match).
+ *   k/v_pool     : one layer, [num_slots, KVH, D] with (slot, head) strides.
+ * dtype DSP_BF16 / DSP_F16; D in {32, 64, 128, 256}; all strides multiples of 8 elements
+ * and all pointers 16-byte aligned. */
+int dsp_qk_norm_rope_append(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                            const void* k, int64_t k_stride_t, int64_t k_stride_h,
+                            const void* v, int64_t v_stride_t, int64_t v_stride_h,
+                            const void* q_norm_weight, const void* k_norm_weight, float eps,
+                            const void* cos_table, const void* sin_table,
+                            int64_t rope_stride_t, const int64_t* slots, int64_t T,
+                            int32_t Hq, int32_t KVH, int32_t D, void* q_out,
+                            int64_t q_out_stride_t, int64_t q_out_stride_h, void* k_pool,
+                            void* v_pool, int64_t num_slots, int64_t pool_stride_slot,
+                            int64_t pool_stride_head, int32_t dtype, int32_t* err_count,
+                            dsp_stream_t stream);
+
 /* ------------------------------------------------------------------ roofline probes
  * Measurement helpers with no counterpart in the reference: kernels that calibrate the
  * achieved bandwidth of the decode and byte-moving kernels (bench.py reports them beside

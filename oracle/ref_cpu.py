@@ -22,6 +22,9 @@ How each function is pinned (tests/test_oracle_*.py):
                          q_len=ctx == ordinary causal attention (torch SDPA is_causal)
   rope ................. textbook inverse-frequency formula checked against the
                          Qwen3 rotary module of transformers; strip(apply(x)) == x
+  qk_norm_rope_append .. transformers' Qwen3RMSNorm module, the runner's rotate-half
+                         RoPE and index_copy_ run as torch bf16 ops on the CPU (library
+                         routines); closed forms (unit weight + zero angle = normalise only)
   layer_map / map ...... known-answer feature order (tests/test_kv_transfer.py:89-100),
                          factored == dense (:103-109), residual formula (:112-126),
                          identity map reproduces its input (:234-252)
@@ -169,6 +172,41 @@ def mq_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, slot_l
         out[off:off + ql] = np.einsum("hqn,nhd->qhd", p, v)
         off += ql
     return out
+
+
+# ------------------------------------------------- attention prologue (model_runner.py)
+
+
+def rms_norm_bf16(x_bits: np.ndarray, w_bits: np.ndarray, eps: float) -> np.ndarray:
+    """Qwen3RMSNorm on bf16 rows (transformers' modeling_qwen3, as q_norm / k_norm at
+    model_runner.py:142-144): var = mean(x^2) in fp32, bf16(x * rsqrt(var + eps)), times the
+    bf16 weight rounded to bf16.  Returns bf16-representable float32."""
+    x = bf16_to_f32(x_bits)
+    var = np.mean(x * x, axis=-1, keepdims=True, dtype=np.float32)
+    inv = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
+    return round_bf16(bf16_to_f32(w_bits) * round_bf16((x * inv).astype(np.float32)))
+
+
+def rope_bf16(x: np.ndarray, cos_bits: np.ndarray, sin_bits: np.ndarray) -> np.ndarray:
+    """The runner's _apply_rope on bf16 tensors (model_runner.py:49-50, 145-146):
+    x * cos + rotate_half(x) * sin with cos/sin (T, D) broadcast over heads, each product
+    and the sum rounded to bf16.  x: (T, H, D) bf16-representable float32."""
+    c, s = bf16_to_f32(cos_bits)[:, None, :], bf16_to_f32(sin_bits)[:, None, :]
+    return round_bf16(round_bf16(x * c) + round_bf16(_rotate_half(x) * s))
+
+
+def qk_norm_rope_append(q_bits, k_bits, v_bits, qw_bits, kw_bits, eps, cos_bits, sin_bits,
+                        slots, k_pool_bits, v_pool_bits) -> np.ndarray:
+    """ModelRunner._attention between projections and attention (model_runner.py:142-148):
+    optional q_norm / k_norm (weights None: none), RoPE on q and k, cache.write(k, v).
+    Writes the pools in place (bf16 bits) and returns the rotated q as bf16 bits."""
+    q, k = bf16_to_f32(q_bits), bf16_to_f32(k_bits)
+    if qw_bits is not None:
+        q, k = rms_norm_bf16(q_bits, qw_bits, eps), rms_norm_bf16(k_bits, kw_bits, eps)
+    q, k = rope_bf16(q, cos_bits, sin_bits), rope_bf16(k, cos_bits, sin_bits)
+    append(k_pool_bits, slots, f32_to_bf16(k))
+    append(v_pool_bits, slots, np.asarray(v_bits, dtype=np.uint16))
+    return f32_to_bf16(q)
 
 
 # ------------------------------------------------------------------ RoPE (transfer.py)

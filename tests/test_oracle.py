@@ -275,3 +275,64 @@ def test_bf16_map_identity_reproduces_input_and_matches_torch_rounding():
     x = v[[2, 0]].permute(1, 0, 2, 3).reshape(T, -1)
     y = (x.double() @ W.double()).float().to(torch.bfloat16) + b     # exact GEMM, bf16 add
     assert np.array_equal(vm[0], _u16(y.view(T, H, D)))
+
+
+def _prologue_inputs(T=5, Hq=4, KVH=2, D=64, seed=50):
+    g = gen(seed)
+    q = torch.randn((T, Hq, D), generator=g).to(torch.bfloat16)
+    k = torch.randn((T, KVH, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((T, KVH, D), generator=g).to(torch.bfloat16)
+    wq = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    wk = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    pos = torch.arange(100, 100 + T)
+    cos_f, sin_f = ref_cpu.rope_tables(pos.numpy(), D, 1e6)
+    cos = torch.from_numpy(cos_f).to(torch.bfloat16)
+    sin = torch.from_numpy(sin_f).to(torch.bfloat16)
+    return q, k, v, wq, wk, cos, sin
+
+
+def test_prologue_matches_torch_ops():
+    """qk_norm_rope_append == transformers' Qwen3RMSNorm + the runner's _apply_rope +
+    index_copy_, run as torch bf16 ops (model_runner.py:142-148).  The variance is an fp32
+    reduction whose summation order differs, so a rare element may round the other way."""
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+    q, k, v, wq, wk, cos, sin = _prologue_inputs()
+    T, Hq, D = q.shape
+    qn, kn = Qwen3RMSNorm(D, eps=1e-6).to(torch.bfloat16), Qwen3RMSNorm(D, eps=1e-6).to(torch.bfloat16)
+    qn.weight.data.copy_(wq)
+    kn.weight.data.copy_(wk)
+
+    def rope(x):
+        x1, x2 = x.chunk(2, dim=-1)
+        return x * cos.unsqueeze(1) + torch.cat((-x2, x1), dim=-1) * sin.unsqueeze(1)
+
+    slots = torch.tensor([7, 0, 12, 3, 9])
+    kpool = torch.randn((16, 2, D), generator=gen(51)).to(torch.bfloat16)
+    vpool = torch.randn((16, 2, D), generator=gen(52)).to(torch.bfloat16)
+    with torch.no_grad():
+        tq, tk = rope(qn(q)), rope(kn(k))
+        tkp, tvp = kpool.clone(), vpool.clone()
+        tkp.index_copy_(0, slots, tk)
+        tvp.index_copy_(0, slots, v)
+    ok, ov = _u16(kpool), _u16(vpool)
+    oq = ref_cpu.qk_norm_rope_append(_u16(q), _u16(k), _u16(v), _u16(wq), _u16(wk), 1e-6,
+                                     _u16(cos), _u16(sin), slots.numpy(), ok, ov)
+    for got, want in ((oq, _u16(tq)), (ok, _u16(tkp))):
+        same = float((got == want).mean())
+        err = np.abs(ref_cpu.bf16_to_f32(got) - ref_cpu.bf16_to_f32(want))
+        ulp = np.abs(ref_cpu.bf16_to_f32(want)) * 2.0 ** -7 + 1e-30
+        assert same >= 0.999 and (err <= ulp).all(), f"identical {same:.4f}"
+    assert np.array_equal(ov, _u16(tvp))
+
+    # no norm (Qwen2): rope only; unit weights and zero angle: normalise only
+    ok2, ov2 = _u16(kpool), _u16(vpool)
+    oq2 = ref_cpu.qk_norm_rope_append(_u16(q), _u16(k), _u16(v), None, None, 1e-6, _u16(cos),
+                                      _u16(sin), slots.numpy(), ok2, ov2)
+    assert np.array_equal(oq2, _u16(rope(q)))
+    ones = _u16(torch.ones(D, dtype=torch.bfloat16))
+    c0, s0 = _u16(torch.ones((T, D), dtype=torch.bfloat16)), _u16(torch.zeros((T, D), dtype=torch.bfloat16))
+    oq3 = ref_cpu.qk_norm_rope_append(_u16(q), _u16(k), _u16(v), ones, ones, 1e-6, c0, s0,
+                                      slots.numpy(), _u16(kpool), _u16(vpool))
+    x = q.float().numpy()
+    want = x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6)
+    assert np.allclose(ref_cpu.bf16_to_f32(oq3), want, rtol=2 ** -7, atol=1e-6)
