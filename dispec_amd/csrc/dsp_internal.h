@@ -32,4 +32,21 @@ int balanced_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
                     float* workspace, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
                     bool f16, int32_t* err_count, hipStream_t s);
 
+// Long query blocks (chunked prefill) on the 128-row FlashAttention-style tile
+// (paged_prefill.hip): the semantics, arguments and workspace layout of
+// dsp_paged_mq_attention, whose entry point has validated them and routes here when
+// `prefill_applies`; partial results go to the 16-row-tile layout its merge kernel reads
+// (tiles16_max 16-row tiles per (sequence, KV head)).  P must be a multiple of 64.
+bool prefill_applies(int32_t D, int32_t block_size, int64_t max_rows);
+int64_t prefill_tiles(int32_t max_q_len, int32_t G);
+int prefill_attention(const uint16_t* q, int64_t q_stride_t, int64_t q_stride_h,
+                      const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,
+                      int64_t kv_stride_slot, int64_t kv_stride_head, const int32_t* block_table,
+                      int64_t bt_stride, int32_t log2_bs, const int32_t* cu_q,
+                      const int32_t* ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t D,
+                      float scale_log2, int32_t max_q_len, int32_t max_ctx, int32_t P,
+                      int32_t num_parts, int32_t tiles16_max, float* ws_acc, float* ws_ml,
+                      uint16_t* out, int64_t o_stride_t, int64_t o_stride_h, bool f16,
+                      int32_t* err_count, hipStream_t s);
+
 }  // namespace dsp_detail

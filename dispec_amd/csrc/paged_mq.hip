@@ -425,11 +425,17 @@ int mq_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const u
 extern "C" int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH,
                                              int32_t max_q_len, int32_t max_ctx) {
   if (B <= 0 || KVH <= 0 || Hq % KVH != 0 || max_q_len <= 0 || max_ctx <= 0) return 128;
-  const int64_t base = int64_t(B) * KVH * mq_tiles(max_q_len, Hq / KVH);
+  const int G = Hq / KVH;
   const int64_t whole = (int64_t(max_ctx) + 127) / 128 * 128;
-  if (base >= 1024) return static_cast<int32_t>(whole);
-  // Aim at ~2048 workgroups, partitions of at least 128 keys (one step of every wave).
-  int64_t want = (2048 + base - 1) / base;
+  // Long query blocks run on the 128-row prefill tile (two resident per CU): aim at ~1024
+  // of them.  Short ones run on 16-row tiles: ~2048.
+  const bool long_q = int64_t(max_q_len) * G >= 128;
+  const int64_t base = int64_t(B) * KVH *
+                       (long_q ? dsp_detail::prefill_tiles(max_q_len, G) : mq_tiles(max_q_len, G));
+  const int64_t target = long_q ? 1024 : 2048;
+  if (base >= target / 2) return static_cast<int32_t>(whole);
+  // Partitions of at least 128 keys (one step of every wave of the 16-row kernel).
+  int64_t want = (target + base - 1) / base;
   if (want > kMaxParts) want = kMaxParts;
   int64_t P = (max_ctx + want - 1) / want;
   P = (P + 127) / 128 * 128;
@@ -499,7 +505,13 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
   const int32_t lbs = dsp_log2i(block_size);
   const int32_t tm = static_cast<int32_t>(tiles);
   int st;
-  if (dtype == DSP_BF16)
+  if (dsp_detail::prefill_applies(D, block_size, int64_t(max_q_len) * G))
+    st = dsp_detail::prefill_attention(qh, q_stride_t, q_stride_h, kh, vh, num_slots,
+                                       kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs,
+                                       cu_q, ctx_lens, B, KVH, G, D, scale_log2, max_q_len, max_ctx,
+                                       P, num_parts, tm, ws_acc, ws_ml, oh, o_stride_t, o_stride_h,
+                                       dtype == DSP_F16, err_count, s);
+  else if (dtype == DSP_BF16)
     st = launch_mq<Bf16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
                             kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
                             ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, ws_acc, ws_ml,

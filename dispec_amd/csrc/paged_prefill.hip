@@ -1,0 +1,327 @@
+// J4 for long query blocks (chunked prefill over the paged cache): a FlashAttention-style
+// tile of 128 packed rows per workgroup on v_mfma_f32_32x32x16.
+//
+// Semantics are dsp_paged_mq_attention's (ModelRunner._attention's native branch,
+// dispec/engine/model_runner.py:160-185): per sequence, SDPA over the paged context with
+// causal_lower_right(q_len, ctx) and GQA; packed row r of a (sequence, KV head) is query
+// r / G of query head kvh*G + r % G.
+//
+// Why a second kernel: the multi-query kernel of paged_mq.hip gives each workgroup 16 rows
+// and streams K/V through registers, which suits verify (q_len <= 16 / G) but caps a
+// 512-token prefill chunk at ~200 TFLOP/s: every 16-row tile re-reads the whole context
+// from L2 (16 flop per K/V byte).  Here four waves share each 64-key chunk of K and V,
+// loaded once per workgroup straight into LDS (global_load_lds_dwordx4, double-buffered,
+// 64 KiB: two workgroups per CU), so a chunk feeds 128 rows.
+//
+// Per wave (32 rows) and chunk:
+//  * S^T = K . Q^T: 2 (keys) x D/16 (dims) MFMAs 32x32x16; K rows come from LDS as the A
+//    operand (16-byte chunks XOR-swizzled by row: conflict-free), Q^T stays in registers.
+//  * Lane l holds row l % 32 and, per 16-key step, keys 4*(l/32) + {0..3, 8..11} -- exactly
+//    the B operand of O^T += V^T . P^T for a 16-key step whose K index is permuted the same
+//    way, so P never leaves registers; V^T is read from LDS 2 bytes at a time in that
+//    order (rows swizzled so the two lane groups hit different banks).
+//  * Online softmax in base 2 per row; the row max needs one exchange between the lane
+//    halves.
+// Partials go to the multi-query kernel's workspace layout (16-row tiles), so its merge
+// kernel combines the key partitions.
+#include <float.h>
+
+#include "dsp_common.h"
+#include "dsp_internal.h"
+#include "dsp_mfma.h"
+
+namespace {
+
+using namespace dsp_mfma;
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWaves = 4, kThreads = 64 * kWaves;
+constexpr int kRows = 32 * kWaves;  // packed rows per workgroup
+constexpr int kChunk = 64;          // keys per LDS chunk
+
+template <typename Tag>
+__device__ __forceinline__ f32x16 mfma32x32(dsp_u32x4 a, dsp_u32x4 b, f32x16 c) {
+  if constexpr (std::is_same<Tag, Bf16Tag>::value)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <typename Tag, int D>
+__global__ __launch_bounds__(kThreads) void paged_prefill_kernel(
+    const uint16_t* __restrict__ q, int64_t qst, int64_t qsh, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
+    const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
+    const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
+    int32_t G, float scale_log2, int32_t P, int32_t num_parts, int32_t tiles16_max,
+    float* __restrict__ ws_acc, float* __restrict__ ws_ml, uint16_t* __restrict__ out,
+    int64_t ost, int64_t osh, int32_t* __restrict__ err_count) {
+  constexpr int NKS = D / 16;        // 16-dim steps of the score MFMA
+  constexpr int NDT = D / 32;        // 32-dim output tiles
+  constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
+  constexpr int ROWB = 2 * D;        // bytes per K/V row
+  constexpr int SLAB = kChunk * ROWB;            // one K (or V) chunk
+  constexpr int RPI = 1024 / ROWB;               // rows per 1-KiB DMA load
+  constexpr int LPW = SLAB / 1024 / kWaves;      // DMA loads per wave per slab
+  static_assert(LPW >= 1, "every wave loads part of a chunk");
+  __shared__ __attribute__((aligned(1024))) char lds[2][2][SLAB];  // [buffer][K | V]
+
+  // heaviest tiles (the last rows see the most keys) are dispatched first
+  const int ntiles = gridDim.x / num_parts;
+  const int part = blockIdx.x % num_parts, tile = ntiles - 1 - int(blockIdx.x / num_parts);
+  const int kvh = blockIdx.y, b = blockIdx.z, KVH = gridDim.y;
+  const int q0 = cu_q[b], qlen = cu_q[b + 1] - q0;
+  const int ctx = ctx_lens[b];
+  const int rows = qlen * G;
+  const int r0 = tile * kRows;
+  if (qlen <= 0 || r0 >= rows) return;
+  if (ctx > max_ctx || ctx < qlen) {  // bad lengths: counted once, the rows are zeros
+    if (part != 0) return;
+    if (threadIdx.x == 0 && tile == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
+    for (int i = threadIdx.x; i < kRows * D; i += kThreads) {
+      const int rr = r0 + i / D;
+      if (rr < rows)
+        out[int64_t(q0 + rr / G) * ost + int64_t(kvh * G + rr % G) * osh + i % D] = 0;
+    }
+    return;
+  }
+  const int r_last = min(r0 + kRows - 1, rows - 1);
+  const int kend = ctx - qlen + r_last / G + 1;  // keys any row of the tile sees
+  const int kbeg = part * P;
+  if (kbeg >= kend) return;
+  const int kfin = min(kbeg + P, kend);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hl = lane >> 5;        // lane half: key sub-range of the operands
+  const int col = lane & 31;       // this lane's row within the wave
+  const int r = r0 + 32 * wave + col;
+  const bool row_ok = r < rows;
+  const int qi = row_ok ? r / G : 0;
+  const int h = kvh * G + (row_ok ? r % G : 0);
+  const int pos_q = ctx - qlen + qi;  // keys 0..pos_q are visible to this row
+  const int64_t bt_row = int64_t(b) * bt_stride;
+  const int64_t head_off = int64_t(kvh) * kvs_head;
+  const int bmask = (1 << log2_bs) - 1;
+
+  // Q^T (B operand): lane holds dims 16*ks + 8*hl .. +8 of its row.
+  dsp_u32x4 qop[NKS];
+#pragma unroll
+  for (int ks = 0; ks < NKS; ++ks)
+    qop[ks] = row_ok ? *reinterpret_cast<const dsp_u32x4*>(q + int64_t(q0 + qi) * qst +
+                                                           int64_t(h) * qsh + 16 * ks + 8 * hl)
+                     : dsp_u32x4{0u, 0u, 0u, 0u};
+
+  // K/V chunk rows into LDS: load j of this wave covers rows (wave*LPW + j)*RPI ..; lane l
+  // fills slot l % CPR of row l / CPR with global chunk slot ^ swz(row).  K rows are
+  // swizzled by (row & (CPR-1)) for the A-operand reads (32 rows, one 16-byte chunk each);
+  // V rows by 4*((row >> 2) & 1): the transposed reads of the two lane halves (rows 4
+  // apart, 64 bytes each) then fall in different bank groups.  Rows past kfin repeat the
+  // last key's row (finite data, masked); an out-of-range slot reads slot 0.
+  auto kswz = [](int row) { return row & (CPR - 1); };
+  auto vswz = [](int row) { return 4 * ((row >> 2) & 1); };
+  auto load_blk = [&](int t0, int32_t (&bl)[LPW]) {
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int key = min(t0 + (wave * LPW + j) * RPI + lane / CPR, kfin - 1);
+      bl[j] = bt[bt_row + (key >> log2_bs)];
+    }
+  };
+  auto issue = [&](int buf, int t0, const int32_t (&bl)[LPW]) {
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const int row = (wave * LPW + j) * RPI + lane / CPR, sl = lane % CPR;
+      const int key = min(t0 + row, kfin - 1);
+      int64_t slot = int64_t(bl[j]) * (bmask + 1) + (key & bmask);
+      slot = (slot >= 0 && slot < num_slots) ? slot : 0;
+      const int64_t e = slot * kvs_slot + head_off;
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(kc + e + 8 * (sl ^ kswz(row))),
+                                       (lds_void_t*)(&lds[buf][0][0] + (wave * LPW + j) * 1024),
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vc + e + 8 * (sl ^ vswz(row))),
+                                       (lds_void_t*)(&lds[buf][1][0] + (wave * LPW + j) * 1024),
+                                       16, 0, 0);
+    }
+  };
+
+  float m = -INFINITY, lpart = 0.f;
+  f32x16 acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
+
+  const int nch = (kfin - kbeg + kChunk - 1) / kChunk;
+  // block ids run one chunk ahead of the DMAs, which run one chunk ahead of the MFMAs
+  int32_t blk[LPW];
+  load_blk(kbeg, blk);
+  issue(0, kbeg, blk);
+  if (nch > 1) load_blk(kbeg + kChunk, blk);
+  for (int c = 0; c < nch; ++c) {
+    const int t0 = kbeg + c * kChunk;
+    // this wave's DMAs of chunk c (and the block ids of chunk c + 1) are in; after the
+    // barrier every wave's are, and every wave is done reading chunk c - 1, whose buffer
+    // the next DMA overwrites
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < nch) {
+      issue((c + 1) & 1, t0 + kChunk, blk);
+      if (c + 2 < nch) load_blk(t0 + 2 * kChunk, blk);
+    }
+    const char* ks_lds = &lds[c & 1][0][0];
+    const char* vs_lds = &lds[c & 1][1][0];
+
+    // ---- scores S^T (keys x rows): two 32-key halves
+    f32x16 sc[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sc[mt][j] = 0.f;
+      const int krow = 32 * mt + col;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const dsp_u32x4 kop = *reinterpret_cast<const dsp_u32x4*>(
+            ks_lds + krow * ROWB + 16 * ((2 * ks + hl) ^ kswz(krow)));
+        sc[mt] = mfma32x32<Tag>(kop, qop[ks], sc[mt]);
+      }
+    }
+    // ---- scale, mask, online softmax.  sc[mt][j] is key 32*mt + 8*(j/4) + 4*hl + j%4.
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int key = t0 + 32 * mt + 8 * (j >> 2) + 4 * hl + (j & 3);
+        const bool ok = row_ok && key <= pos_q && key < kfin;
+        sc[mt][j] = ok ? sc[mt][j] * scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sc[mt][j]);
+      }
+    mx = fmaxf(mx, dsp_shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = dsp_exp2(m - m_use);
+    m = m_new;
+    float psum = 0.f;
+    // P^T operands of the four 16-key steps: step ps = 2*mt + half takes registers
+    // j = 8*half .. 8*half + 7, i.e. keys 16*ps + 4*hl + {0..3, 8..11}.
+    dsp_u32x4 pop[4];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        uint16_t pb[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float p = dsp_exp2(sc[mt][8 * half + i] - m_use);
+          psum += p;
+          pb[i] = narrow<Tag>(p);
+        }
+        pop[2 * mt + half] = dsp_u32x4{pack2(pb[0], pb[1]), pack2(pb[2], pb[3]),
+                                       pack2(pb[4], pb[5]), pack2(pb[6], pb[7])};
+      }
+    lpart = lpart * alpha + psum;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
+
+    // ---- O^T += V^T . P^T: lane reads dim 32*dt + col of keys 16*ps + 4*hl + (i & 3) +
+    // 8*(i >> 2), i < 8 (the P^T key order)
+#pragma unroll
+    for (int ps = 0; ps < 4; ++ps) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int d = 32 * dt + col;
+        uint16_t v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int kr = 16 * ps + 4 * hl + (i & 3) + 8 * (i >> 2);
+          v[i] = *reinterpret_cast<const uint16_t*>(vs_lds + kr * ROWB +
+                                                    16 * ((d >> 3) ^ vswz(kr)) + 2 * (d & 7));
+        }
+        const dsp_u32x4 vop = dsp_u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]),
+                                        pack2(v[6], v[7])};
+        acc[dt] = mfma32x32<Tag>(vop, pop[ps], acc[dt]);
+      }
+    }
+  }
+
+  // ---- epilogue: row sums over the two lane halves; acc[dt][j] = O[row col][dim 32*dt +
+  // 8*(j/4) + 4*hl + j%4]
+  lpart += dsp_shfl_xor(lpart, 32);
+  if (!row_ok) return;
+  const int st = r / 16, rr = r % 16;                    // 16-row tile of the merge layout
+  if (st >= tiles16_max) return;  // q_len past the caller's max_q_len: rows not covered
+  const int r_last16 = min(st * 16 + 15, rows - 1);
+  const int kend16 = ctx - qlen + r_last16 / G + 1;
+  const int nparts16 = (kend16 + P - 1) / P;
+  if (part >= nparts16) return;  // the merge for this 16-row tile does not read this partition
+  if (nparts16 == 1) {
+    const float inv = lpart > 0.f ? 1.f / lpart : 0.f;
+    uint16_t* o = out + int64_t(q0 + qi) * ost + int64_t(h) * osh;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        o[32 * dt + 8 * (j >> 2) + 4 * hl + (j & 3)] = narrow<Tag>(acc[dt][j] * inv);
+    return;
+  }
+  const int64_t slot = ((int64_t(b) * KVH + kvh) * tiles16_max + st) * num_parts + part;
+  float* a = ws_acc + (slot * 16 + rr) * D;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+    for (int j4 = 0; j4 < 4; ++j4)
+      *reinterpret_cast<f32x4*>(a + 32 * dt + 8 * j4 + 4 * hl) =
+          f32x4{acc[dt][4 * j4], acc[dt][4 * j4 + 1], acc[dt][4 * j4 + 2], acc[dt][4 * j4 + 3]};
+  if (hl == 0) {
+    ws_ml[2 * (slot * 16 + rr)] = m;
+    ws_ml[2 * (slot * 16 + rr) + 1] = lpart;
+  }
+}
+
+}  // namespace
+
+namespace dsp_detail {
+
+bool prefill_applies(int32_t D, int32_t block_size, int64_t max_rows) {
+  return (D == 64 || D == 128) && block_size >= 16 && max_rows >= kRows;
+}
+
+int64_t prefill_tiles(int32_t max_q_len, int32_t G) {
+  return (int64_t(max_q_len) * G + kRows - 1) / kRows;
+}
+
+int prefill_attention(const uint16_t* q, int64_t q_stride_t, int64_t q_stride_h,
+                      const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,
+                      int64_t kv_stride_slot, int64_t kv_stride_head, const int32_t* block_table,
+                      int64_t bt_stride, int32_t log2_bs, const int32_t* cu_q,
+                      const int32_t* ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t D,
+                      float scale_log2, int32_t max_q_len, int32_t max_ctx, int32_t P,
+                      int32_t num_parts, int32_t tiles16_max, float* ws_acc, float* ws_ml,
+                      uint16_t* out, int64_t o_stride_t, int64_t o_stride_h, bool f16,
+                      int32_t* err_count, hipStream_t s) {
+  const int64_t tiles = prefill_tiles(max_q_len, G);
+  dim3 grid(static_cast<unsigned>(tiles * num_parts), static_cast<unsigned>(KVH),
+            static_cast<unsigned>(B));
+#define DSP_PREFILL_ARGS                                                                     \
+  q, q_stride_t, q_stride_h, k_cache, v_cache, num_slots, kv_stride_slot, kv_stride_head,    \
+      block_table, bt_stride, log2_bs, cu_q, ctx_lens, max_ctx, G, scale_log2, P, num_parts, \
+      tiles16_max, ws_acc, ws_ml, out, o_stride_t, o_stride_h, err_count
+  if (D == 128) {
+    if (f16) paged_prefill_kernel<F16Tag, 128><<<grid, kThreads, 0, s>>>(DSP_PREFILL_ARGS);
+    else paged_prefill_kernel<Bf16Tag, 128><<<grid, kThreads, 0, s>>>(DSP_PREFILL_ARGS);
+  } else {
+    if (f16) paged_prefill_kernel<F16Tag, 64><<<grid, kThreads, 0, s>>>(DSP_PREFILL_ARGS);
+    else paged_prefill_kernel<Bf16Tag, 64><<<grid, kThreads, 0, s>>>(DSP_PREFILL_ARGS);
+  }
+#undef DSP_PREFILL_ARGS
+  return dsp_launch_status();
+}
+
+}  // namespace dsp_detail
