@@ -51,9 +51,11 @@ __device__ __forceinline__ f32x16 mfma32x32(dsp_u32x4 a, dsp_u32x4 b, f32x16 c) 
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 
 template <typename Tag, int D>
-__global__ __launch_bounds__(kThreads) void paged_prefill_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t qst, int64_t qsh, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
     const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
@@ -104,7 +106,11 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(
   const bool row_ok = r < rows;
   const int qi = row_ok ? r / G : 0;
   const int h = kvh * G + (row_ok ? r % G : 0);
-  const int pos_q = ctx - qlen + qi;  // keys 0..pos_q are visible to this row
+  // Keys 0..lim are visible to this row (causal limit, and the partition's end); lim_min
+  // is the smallest limit among the wave's rows (its first row), wave-uniform.  Rows past
+  // `rows` have q = 0: finite scores, never stored.
+  const int lim = min(ctx - qlen + qi, kfin - 1);
+  const int lim_min = min(ctx - qlen + (r0 + 32 * wave) / G, kfin - 1);
   const int64_t bt_row = int64_t(b) * bt_stride;
   const int64_t head_off = int64_t(kvh) * kvs_head;
   const int bmask = (1 << log2_bs) - 1;
@@ -120,11 +126,12 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(
   // K/V chunk rows into LDS: load j of this wave covers rows (wave*LPW + j)*RPI ..; lane l
   // fills slot l % CPR of row l / CPR with global chunk slot ^ swz(row).  K rows are
   // swizzled by (row & (CPR-1)) for the A-operand reads (32 rows, one 16-byte chunk each);
-  // V rows by 4*((row >> 2) & 1): the transposed reads of the two lane halves (rows 4
-  // apart, 64 bytes each) then fall in different bank groups.  Rows past kfin repeat the
-  // last key's row (finite data, masked); an out-of-range slot reads slot 0.
+  // V rows by whole 64-byte groups (4 chunks): 4*(row & 3) at D 128 and 4*((row >> 1) & 1)
+  // at D 64, so each half-wave of a transposing read (4 consecutive rows x 64 bytes) covers
+  // all 64 banks once.  Rows past kfin repeat the last key's row (finite data, masked);
+  // an out-of-range slot reads slot 0.
   auto kswz = [](int row) { return row & (CPR - 1); };
-  auto vswz = [](int row) { return 4 * ((row >> 2) & 1); };
+  auto vswz = [](int row) { return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1); };
   auto load_blk = [&](int t0, int32_t (&bl)[LPW]) {
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
@@ -171,12 +178,36 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
+    const char* ks_lds = &lds[c & 1][0][0];
+    const char* vs_lds = &lds[c & 1][1][0];
+
+    // V^T operands of the whole chunk first: the compiler makes a transposing LDS read wait
+    // for every LDS DMA in flight, so they are issued before the next chunk's DMAs.
+    // O^T += V^T . P^T takes, per 16-key step ps, the V^T operand dim 32*dt + col, K index
+    // 8*hl + i <-> key 16*ps + 8*(i/4) + 4*hl + i%4.  In ds_read_b64_tr_b16, lane g + 4a + e
+    // of each 16-lane group g receives element e of the 4-element segments addressed by
+    // lanes g + a + 4j (j = 0..3); so lane s addresses key 16*ps + 8*inst + 4*hl +
+    // (s%16)/4, dims 32*dt + 16*((s/16)%2) + 4*(s%4) .. +3.
+    dsp_u32x4 vop[4][NDT];
+#pragma unroll
+    for (int ps = 0; ps < 4; ++ps) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        v4i16 vh[2];
+#pragma unroll
+        for (int inst = 0; inst < 2; ++inst) {
+          const int kr = 16 * ps + 8 * inst + 4 * hl + ((lane & 15) >> 2);
+          const int dim0 = 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+          vh[inst] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(
+              vs_lds + kr * ROWB + 16 * ((dim0 >> 3) ^ vswz(kr)) + 2 * (dim0 & 7)));
+        }
+        vop[ps][dt] = __builtin_bit_cast(dsp_u32x4, vh);
+      }
+    }
     if (c + 1 < nch) {
       issue((c + 1) & 1, t0 + kChunk, blk);
       if (c + 2 < nch) load_blk(t0 + 2 * kChunk, blk);
     }
-    const char* ks_lds = &lds[c & 1][0][0];
-    const char* vs_lds = &lds[c & 1][1][0];
 
     // ---- scores S^T (keys x rows): two 32-key halves
     f32x16 sc[2];
@@ -192,23 +223,34 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(
         sc[mt] = mfma32x32<Tag>(kop, qop[ks], sc[mt]);
       }
     }
-    // ---- scale, mask, online softmax.  sc[mt][j] is key 32*mt + 8*(j/4) + 4*hl + j%4.
+    // ---- mask (only chunks that reach past a row's causal limit or past kfin), row max.
+    // sc[mt][j] is key 32*mt + 8*(j/4) + 4*hl + j%4 of this lane's row.
+    if (t0 + kChunk - 1 > lim_min) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int key = t0 + 32 * mt + 8 * (j >> 2) + 4 * hl + (j & 3);
+          sc[mt][j] = key <= lim ? sc[mt][j] : -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int key = t0 + 32 * mt + 8 * (j >> 2) + 4 * hl + (j & 3);
-        const bool ok = row_ok && key <= pos_q && key < kfin;
-        sc[mt][j] = ok ? sc[mt][j] * scale_log2 : -INFINITY;
-        mx = fmaxf(mx, sc[mt][j]);
-      }
-    mx = fmaxf(mx, dsp_shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = dsp_exp2(m - m_use);
-    m = m_new;
-    float psum = 0.f;
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sc[mt][j]);
+    mx = fmaxf(mx, dsp_shfl_xor(mx, 32)) * scale_log2;  // base-2 units; -inf stays -inf
+    // Lazy rescale: the running max m only moves when some row's chunk max exceeds it by
+    // more than 8 (so p <= 2^8); the result is exact either way, since l and acc share m.
+    if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = m_new == -INFINITY ? 1.f : dsp_exp2(m - m_new);
+      m = m_new;
+      lpart *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
+    }
+    const float neg_m = m == -INFINITY ? 0.f : -m;
     // P^T operands of the four 16-key steps: step ps = 2*mt + half takes registers
     // j = 8*half .. 8*half + 7, i.e. keys 16*ps + 4*hl + {0..3, 8..11}.
     dsp_u32x4 pop[4];
@@ -219,36 +261,19 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(
         uint16_t pb[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float p = dsp_exp2(sc[mt][8 * half + i] - m_use);
-          psum += p;
+          const float p = dsp_exp2(fmaf(sc[mt][8 * half + i], scale_log2, neg_m));
+          lpart += p;
           pb[i] = narrow<Tag>(p);
         }
         pop[2 * mt + half] = dsp_u32x4{pack2(pb[0], pb[1]), pack2(pb[2], pb[3]),
                                        pack2(pb[4], pb[5]), pack2(pb[6], pb[7])};
       }
-    lpart = lpart * alpha + psum;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
 
-    // ---- O^T += V^T . P^T: lane reads dim 32*dt + col of keys 16*ps + 4*hl + (i & 3) +
-    // 8*(i >> 2), i < 8 (the P^T key order)
+    // ---- O^T += V^T . P^T
 #pragma unroll
-    for (int ps = 0; ps < 4; ++ps) {
+    for (int ps = 0; ps < 4; ++ps)
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const int d = 32 * dt + col;
-        uint16_t v[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int kr = 16 * ps + 4 * hl + (i & 3) + 8 * (i >> 2);
-          v[i] = *reinterpret_cast<const uint16_t*>(vs_lds + kr * ROWB +
-                                                    16 * ((d >> 3) ^ vswz(kr)) + 2 * (d & 7));
-        }
-        const dsp_u32x4 vop = dsp_u32x4{pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]),
-                                        pack2(v[6], v[7])};
-        acc[dt] = mfma32x32<Tag>(vop, pop[ps], acc[dt]);
-      }
-    }
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma32x32<Tag>(vop[ps][dt], pop[ps], acc[dt]);
   }
 
   // ---- epilogue: row sums over the two lane halves; acc[dt][j] = O[row col][dim 32*dt +
