@@ -37,7 +37,8 @@ int balanced_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
 // dsp_paged_mq_attention, whose entry point has validated them and routes here when
 // `prefill_applies`; partial results go to the 16-row-tile layout its merge kernel reads
 // (tiles16_max 16-row tiles per (sequence, KV head)).  P must be a multiple of 64.
-bool prefill_applies(int32_t D, int32_t block_size, int64_t max_rows);
+bool prefill_applies(int32_t D, int32_t block_size, int64_t max_rows, int64_t num_slots,
+                     int64_t kv_stride_slot);
 int64_t prefill_tiles(int32_t max_q_len, int32_t G);
 int prefill_attention(const uint16_t* q, int64_t q_stride_t, int64_t q_stride_h,
                       const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,

@@ -505,7 +505,8 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
   const int32_t lbs = dsp_log2i(block_size);
   const int32_t tm = static_cast<int32_t>(tiles);
   int st;
-  if (dsp_detail::prefill_applies(D, block_size, int64_t(max_q_len) * G))
+  if (dsp_detail::prefill_applies(D, block_size, int64_t(max_q_len) * G, num_slots,
+                                  kv_stride_slot))
     st = dsp_detail::prefill_attention(qh, q_stride_t, q_stride_h, kh, vh, num_slots,
                                        kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs,
                                        cu_q, ctx_lens, B, KVH, G, D, scale_log2, max_q_len, max_ctx,

@@ -132,25 +132,35 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // an out-of-range slot reads slot 0.
   auto kswz = [](int row) { return row & (CPR - 1); };
   auto vswz = [](int row) { return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1); };
-  auto load_blk = [&](int t0, int32_t (&bl)[LPW]) {
+  // Wave w loads rows 16*w .. 16*w + 15 of each chunk.  Chunks start at multiples of 64
+  // keys and blocks hold a multiple of 16 tokens, so those rows lie in one block: its id
+  // is wave-uniform and the addresses are a scalar base plus per-lane constants.  Rows past
+  // kfin read other slots of the same block (finite data, masked); an out-of-range block
+  // reads slots 0..15.
+  static_assert(LPW * RPI == 16, "16 rows per wave per chunk");
+  uint32_t koff[LPW], voff[LPW];
 #pragma unroll
-    for (int j = 0; j < LPW; ++j) {
-      const int key = min(t0 + (wave * LPW + j) * RPI + lane / CPR, kfin - 1);
-      bl[j] = bt[bt_row + (key >> log2_bs)];
-    }
+  for (int j = 0; j < LPW; ++j) {
+    const int rw = j * RPI + lane / CPR, row = 16 * wave + rw, sl = lane % CPR;
+    koff[j] = uint32_t(rw * kvs_slot * 2 + 16 * (sl ^ kswz(row)));
+    voff[j] = uint32_t(rw * kvs_slot * 2 + 16 * (sl ^ vswz(row)));
+  }
+  auto load_blk = [&](int t0) {
+    return bt[bt_row + (min(t0 + 16 * wave, kfin - 1) >> log2_bs)];
   };
-  auto issue = [&](int buf, int t0, const int32_t (&bl)[LPW]) {
+  auto issue = [&](int buf, int t0, int32_t blk_v) {
+    const int32_t blk = __builtin_amdgcn_readfirstlane(blk_v);
+    int64_t slot0 = int64_t(blk) * (bmask + 1) + ((t0 + 16 * wave) & bmask);
+    if (blk < 0 || (int64_t(blk) + 1) * (bmask + 1) > num_slots) slot0 = 0;
+    const int64_t e = slot0 * kvs_slot + head_off;
+    const char* kb = reinterpret_cast<const char*>(kc + e);
+    const char* vb = reinterpret_cast<const char*>(vc + e);
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const int row = (wave * LPW + j) * RPI + lane / CPR, sl = lane % CPR;
-      const int key = min(t0 + row, kfin - 1);
-      int64_t slot = int64_t(bl[j]) * (bmask + 1) + (key & bmask);
-      slot = (slot >= 0 && slot < num_slots) ? slot : 0;
-      const int64_t e = slot * kvs_slot + head_off;
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(kc + e + 8 * (sl ^ kswz(row))),
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(kb + koff[j]),
                                        (lds_void_t*)(&lds[buf][0][0] + (wave * LPW + j) * 1024),
                                        16, 0, 0);
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vc + e + 8 * (sl ^ vswz(row))),
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + voff[j]),
                                        (lds_void_t*)(&lds[buf][1][0] + (wave * LPW + j) * 1024),
                                        16, 0, 0);
     }
@@ -165,10 +175,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 
   const int nch = (kfin - kbeg + kChunk - 1) / kChunk;
   // block ids run one chunk ahead of the DMAs, which run one chunk ahead of the MFMAs
-  int32_t blk[LPW];
-  load_blk(kbeg, blk);
+  int32_t blk = load_blk(kbeg);
   issue(0, kbeg, blk);
-  if (nch > 1) load_blk(kbeg + kChunk, blk);
+  if (nch > 1) blk = load_blk(kbeg + kChunk);
   for (int c = 0; c < nch; ++c) {
     const int t0 = kbeg + c * kChunk;
     // this wave's DMAs of chunk c (and the block ids of chunk c + 1) are in; after the
@@ -206,7 +215,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     }
     if (c + 1 < nch) {
       issue((c + 1) & 1, t0 + kChunk, blk);
-      if (c + 2 < nch) load_blk(t0 + 2 * kChunk, blk);
+      if (c + 2 < nch) blk = load_blk(t0 + 2 * kChunk);
     }
 
     // ---- scores S^T (keys x rows): two 32-key halves
@@ -314,8 +323,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 
 namespace dsp_detail {
 
-bool prefill_applies(int32_t D, int32_t block_size, int64_t max_rows) {
-  return (D == 64 || D == 128) && block_size >= 16 && max_rows >= kRows;
+bool prefill_applies(int32_t D, int32_t block_size, int64_t max_rows, int64_t num_slots,
+                     int64_t kv_stride_slot) {
+  return (D == 64 || D == 128) && block_size >= 16 && max_rows >= kRows && num_slots >= 16 &&
+         kv_stride_slot < (int64_t(1) << 25);  // 16-row lane offsets fit 32 bits
 }
 
 int64_t prefill_tiles(int32_t max_q_len, int32_t G) {
