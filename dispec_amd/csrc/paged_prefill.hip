@@ -73,10 +73,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   static_assert(LPW >= 1, "every wave loads part of a chunk");
   __shared__ __attribute__((aligned(1024))) char lds[2][2][SLAB];  // [buffer][K | V]
 
-  // heaviest tiles (the last rows see the most keys) are dispatched first
-  const int ntiles = gridDim.x / num_parts;
-  const int part = blockIdx.x % num_parts, tile = ntiles - 1 - int(blockIdx.x / num_parts);
-  const int kvh = blockIdx.y, b = blockIdx.z, KVH = gridDim.y;
+  // XCD-aware order: the dispatcher hands workgroup `lin` to XCD lin % 8.  Each XCD gets a
+  // contiguous range of logical ids, so the tiles of one (sequence, KV head) -- which read
+  // the same K/V -- run on one XCD and share its L2.  Within a (sequence, KV head) the
+  // heaviest tiles (the last rows see the most keys) come first.
+  const int X = gridDim.x, KVH = gridDim.y;
+  const int64_t nwg = int64_t(X) * KVH * gridDim.z;
+  const int64_t lin = blockIdx.x + int64_t(X) * (blockIdx.y + int64_t(KVH) * blockIdx.z);
+  const int64_t q8 = nwg / 8, r8 = nwg % 8, xcd = lin % 8, pos = lin / 8;
+  const int64_t lg = xcd < r8 ? xcd * (q8 + 1) + pos : r8 * (q8 + 1) + (xcd - r8) * q8 + pos;
+  const int xl = int(lg % X);
+  const int kvh = int((lg / X) % KVH), b = int(lg / X / KVH);
+  const int ntiles = X / num_parts;
+  const int part = xl % num_parts, tile = ntiles - 1 - xl / num_parts;
   const int q0 = cu_q[b], qlen = cu_q[b + 1] - q0;
   const int ctx = ctx_lens[b];
   const int rows = qlen * G;
