@@ -51,6 +51,21 @@ __device__ __forceinline__ f32x16 mfma32x32(dsp_u32x4 a, dsp_u32x4 b, f32x16 c) 
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+
+// One LDS DMA (global_load_lds_dwordx4): 16 bytes per lane from sbase + voff into LDS at
+// m0 + 16 * lane.  It is issued from inline assembly so that the compiler does not make
+// later LDS reads wait for it: its waitcnt pass cannot tell the DMA's target buffer from
+// the one being read and would wait for the whole DMA.  The kernel waits for it itself
+// (vmcnt) before the barrier that publishes the chunk.  M0 has no other user here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(voff), "s"(sbase), "s"(m0)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 
@@ -154,6 +169,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     koff[j] = uint32_t(rw * kvs_slot * 2 + 16 * (sl ^ kswz(row)));
     voff[j] = uint32_t(rw * kvs_slot * 2 + 16 * (sl ^ vswz(row)));
   }
+  const uint32_t lds_base = uint32_t(reinterpret_cast<uintptr_t>((lds_void_t*)&lds[0][0][0]));
   auto load_blk = [&](int t0) {
     return bt[bt_row + (min(t0 + 16 * wave, kfin - 1) >> log2_bs)];
   };
@@ -164,14 +180,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const int64_t e = slot0 * kvs_slot + head_off;
     const char* kb = reinterpret_cast<const char*>(kc + e);
     const char* vb = reinterpret_cast<const char*>(vc + e);
+    const uint32_t m0 = lds_base + uint32_t(buf * 2 * SLAB + wave * LPW * 1024);
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(kb + koff[j]),
-                                       (lds_void_t*)(&lds[buf][0][0] + (wave * LPW + j) * 1024),
-                                       16, 0, 0);
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(vb + voff[j]),
-                                       (lds_void_t*)(&lds[buf][1][0] + (wave * LPW + j) * 1024),
-                                       16, 0, 0);
+      dma16(kb, koff[j], m0 + j * 1024);
+      dma16(vb, voff[j], m0 + SLAB + j * 1024);
     }
   };
 
@@ -196,36 +209,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    const char* ks_lds = &lds[c & 1][0][0];
-    const char* vs_lds = &lds[c & 1][1][0];
-
-    // V^T operands of the whole chunk first: the compiler makes a transposing LDS read wait
-    // for every LDS DMA in flight, so they are issued before the next chunk's DMAs.
-    // O^T += V^T . P^T takes, per 16-key step ps, the V^T operand dim 32*dt + col, K index
-    // 8*hl + i <-> key 16*ps + 8*(i/4) + 4*hl + i%4.  In ds_read_b64_tr_b16, lane g + 4a + e
-    // of each 16-lane group g receives element e of the 4-element segments addressed by
-    // lanes g + a + 4j (j = 0..3); so lane s addresses key 16*ps + 8*inst + 4*hl +
-    // (s%16)/4, dims 32*dt + 16*((s/16)%2) + 4*(s%4) .. +3.
-    dsp_u32x4 vop[4][NDT];
-#pragma unroll
-    for (int ps = 0; ps < 4; ++ps) {
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        v4i16 vh[2];
-#pragma unroll
-        for (int inst = 0; inst < 2; ++inst) {
-          const int kr = 16 * ps + 8 * inst + 4 * hl + ((lane & 15) >> 2);
-          const int dim0 = 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-          vh[inst] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(
-              vs_lds + kr * ROWB + 16 * ((dim0 >> 3) ^ vswz(kr)) + 2 * (dim0 & 7)));
-        }
-        vop[ps][dt] = __builtin_bit_cast(dsp_u32x4, vh);
-      }
-    }
     if (c + 1 < nch) {
       issue((c + 1) & 1, t0 + kChunk, blk);
       if (c + 2 < nch) blk = load_blk(t0 + 2 * kChunk);
     }
+    const char* ks_lds = &lds[c & 1][0][0];
+    const char* vs_lds = &lds[c & 1][1][0];
 
     // ---- scores S^T (keys x rows): two 32-key halves
     f32x16 sc[2];
@@ -287,11 +276,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
                                        pack2(pb[4], pb[5]), pack2(pb[6], pb[7])};
       }
 
-    // ---- O^T += V^T . P^T
+    // ---- O^T += V^T . P^T.  Per 16-key step ps the V^T operand is dim 32*dt + col, K index
+    // 8*hl + i <-> key 16*ps + 8*(i/4) + 4*hl + i%4 (the P^T order).  In ds_read_b64_tr_b16,
+    // lane g + 4a + e of each 16-lane group g receives element e of the 4-element segments
+    // addressed by lanes g + a + 4j (j = 0..3); so lane s addresses key 16*ps + 8*inst +
+    // 4*hl + (s%16)/4, dims 32*dt + 16*((s/16)%2) + 4*(s%4) .. +3, for inst = 0, 1.
 #pragma unroll
-    for (int ps = 0; ps < 4; ++ps)
+    for (int ps = 0; ps < 4; ++ps) {
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) acc[dt] = mfma32x32<Tag>(vop[ps][dt], pop[ps], acc[dt]);
+      for (int dt = 0; dt < NDT; ++dt) {
+        v4i16 vh[2];
+#pragma unroll
+        for (int inst = 0; inst < 2; ++inst) {
+          const int kr = 16 * ps + 8 * inst + 4 * hl + ((lane & 15) >> 2);
+          const int dim0 = 32 * dt + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+          vh[inst] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_t*)(
+              vs_lds + kr * ROWB + 16 * ((dim0 >> 3) ^ vswz(kr)) + 2 * (dim0 & 7)));
+        }
+        acc[dt] = mfma32x32<Tag>(__builtin_bit_cast(dsp_u32x4, vh), pop[ps], acc[dt]);
+      }
+    }
   }
 
   // ---- epilogue: row sums over the two lane halves; acc[dt][j] = O[row col][dim 32*dt +
