@@ -44,7 +44,7 @@ SIGNATURES: dict[str, tuple] = {
                                  _P, c_int64, c_int32, _P, c_int64, _P, c_int32, c_int32,
                                  c_int32, c_int32, c_float, c_int32, c_int32, _P, c_size_t,
                                  _P, c_int64, c_int64, c_int32, _P, _P]),
-    "dsp_paged_mq_partition_tokens": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "dsp_paged_mq_partition_tokens": (c_int, [c_int32] * 6),
     "dsp_paged_mq_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32,
                                                 c_int32, c_int32]),
     "dsp_paged_mq_attention": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64,

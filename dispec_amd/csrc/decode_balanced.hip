@@ -511,6 +511,10 @@ int launch_balanced(int D, A... args) {
   }
 }
 
+}  // namespace
+
+namespace dsp_detail {
+
 int device_cus() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
@@ -520,9 +524,6 @@ int device_cus() {
   return cus;
 }
 
-}  // namespace
-
-namespace dsp_detail {
 
 bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
                              int32_t block_size) {
@@ -535,7 +536,7 @@ bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
 }
 
 int32_t balanced_workers(int32_t B, int32_t KVH, int32_t max_ctx) {
-  const int64_t cap = int64_t(device_cus()) * 4 * kOcc;
+  const int64_t cap = int64_t(dsp_detail::device_cus()) * 4 * kOcc;
   const int64_t cmax = int64_t(B) * KVH * ((int64_t(max_ctx) + 15) >> kLog2Unit);
   int64_t want = (cmax + kMinUnits - 1) / kMinUnits;
   if (want < 1) want = 1;

@@ -5,6 +5,9 @@
 
 namespace dsp_detail {
 
+// Compute units of the current device (256 if the query fails).
+int device_cus();
+
 // Block-table decode on the multi-query MFMA kernel (paged_mq.hip) with q_len 1 per
 // sequence.  The caller (dsp_paged_decode) has validated the arguments; the kernel writes
 // partial results as ws_acc[(b * Hq + h) * num_parts + part][D] and ws_ml[...][2] (row max,

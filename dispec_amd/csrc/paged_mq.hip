@@ -20,6 +20,7 @@
 //  * Softmax is online per packed row in base 2; the row max is combined across the 4
 //    lane groups with two cross-lane exchanges.
 #include <float.h>
+#include <stdint.h>
 
 #include "dsp_common.h"
 #include "dsp_internal.h"
@@ -422,20 +423,36 @@ int mq_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const u
 
 }  // namespace dsp_detail
 
-extern "C" int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH,
+extern "C" int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
                                              int32_t max_q_len, int32_t max_ctx) {
   if (B <= 0 || KVH <= 0 || Hq % KVH != 0 || max_q_len <= 0 || max_ctx <= 0) return 128;
   const int G = Hq / KVH;
   const int64_t whole = (int64_t(max_ctx) + 127) / 128 * 128;
-  // Long query blocks run on the 128-row prefill tile (two resident per CU): aim at ~1024
-  // of them.  Short ones run on 16-row tiles: ~2048.
-  const bool long_q = int64_t(max_q_len) * G >= 128;
-  const int64_t base = int64_t(B) * KVH *
-                       (long_q ? dsp_detail::prefill_tiles(max_q_len, G) : mq_tiles(max_q_len, G));
-  const int64_t target = long_q ? 1024 : 2048;
-  if (base >= target / 2) return static_cast<int32_t>(whole);
-  // Partitions of at least 128 keys (one step of every wave of the 16-row kernel).
-  int64_t want = (target + base - 1) / base;
+  if (int64_t(max_q_len) * G >= 128) {
+    // Long query blocks run on the 128-row prefill tile, two resident per CU at D 128 and
+    // four at D 64 (LDS and registers).  Pick the
+    // partition count n that minimises (rounds of resident tiles) x (keys per tile + a
+    // fixed cost) + the merge's cost per partition, in units of keys: a split pays only
+    // when it fills a round of the machine that would otherwise idle.
+    const int64_t base = int64_t(B) * KVH * dsp_detail::prefill_tiles(max_q_len, G);
+    const int64_t slots = (D <= 64 ? 4 : 2) * int64_t(dsp_detail::device_cus());
+    if (base >= slots) return static_cast<int32_t>(whole);
+    int64_t best_p = whole, best_cost = INT64_MAX;
+    for (int n = 1; n <= kMaxParts; ++n) {
+      const int64_t p = ((max_ctx + n - 1) / n + 127) / 128 * 128;
+      const int64_t parts = (max_ctx + p - 1) / p;
+      if (parts != n) continue;  // the same partition as a smaller n
+      const int64_t rounds = (base * parts + slots - 1) / slots;
+      const int64_t cost = rounds * (p + 256) + (parts > 1 ? 192 + 48 * parts : 0);
+      if (cost < best_cost) best_cost = cost, best_p = p;
+    }
+    return static_cast<int32_t>(best_p);
+  }
+  // Short ones run on 16-row tiles: aim at ~2048 workgroups, partitions of at least 128
+  // keys (one step of every wave).
+  const int64_t base = int64_t(B) * KVH * mq_tiles(max_q_len, G);
+  if (base >= 1024) return static_cast<int32_t>(whole);
+  int64_t want = (2048 + base - 1) / base;
   if (want > kMaxParts) want = kMaxParts;
   int64_t P = (max_ctx + want - 1) / want;
   P = (P + 127) / 128 * 128;
@@ -484,7 +501,7 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
   const int64_t tiles = mq_tiles(max_q_len, G);
   const int P = partition_tokens > 0
                     ? partition_tokens
-                    : dsp_paged_mq_partition_tokens(B, Hq, KVH, max_q_len, max_ctx);
+                    : dsp_paged_mq_partition_tokens(B, Hq, KVH, D, max_q_len, max_ctx);
   DSP_HOST_CHECK(P % 128 == 0, DSP_EINVAL);
   const int num_parts = max_ctx > 0 ? (max_ctx + P - 1) / P : 1;
   DSP_HOST_CHECK(num_parts <= kMaxParts, DSP_EINVAL);

@@ -164,7 +164,7 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
         raise ValueError("out must have q's shape and dtype with head_dim contiguous")
     L = _lib.lib()
-    P = partition_tokens or L.dsp_paged_mq_partition_tokens(B, Hq, KVH, int(max_q_len),
+    P = partition_tokens or L.dsp_paged_mq_partition_tokens(B, Hq, KVH, D, int(max_q_len),
                                                             int(max_ctx))
     need = L.dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, int(max_q_len), int(max_ctx), P)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):

@@ -186,9 +186,12 @@ int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  *                max_ctx); 0 picks one from the shape.  More than one partition needs
  *                `workspace` (dsp_paged_mq_workspace_bytes) and a merge kernel.
  * dtype DSP_BF16 / DSP_F16; D in {32, 64, 128}; any G = Hq / KVH.  A sequence with
- * q_len > ctx or ctx > max_ctx is counted in err_count and its rows written as zeros. */
-int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH, int32_t max_q_len,
-                                  int32_t max_ctx);
+ * q_len > ctx or ctx > max_ctx is counted in err_count and its rows written as zeros.
+ * Batches with max_q_len * G >= 128 (D 64 or 128, blocks of >= 16 tokens) run on a
+ * 128-row tile built for chunked prefill; shorter ones (verify) on 16-row tiles.  The
+ * automatic partition is sized for whichever runs. */
+int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
+                                  int32_t max_q_len, int32_t max_ctx);
 size_t dsp_paged_mq_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
                                     int32_t max_q_len, int32_t max_ctx, int32_t partition_tokens);
 int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,

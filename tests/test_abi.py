@@ -81,6 +81,13 @@ def test_partition_and_workspace_sizing(lib):
     assert lib.dsp_paged_decode_partition_tokens(1, 1, 64, 1000) == 128
     # head_dim 16 stays on the VALU kernel's sizing (power-of-two multiple of 128, <= 512)
     assert lib.dsp_paged_decode_partition_tokens(16, 8, 16, 32768) == 512
+    # multi-query, long query blocks (128-row tiles; 256 CUs assumed without a GPU):
+    # 96 tiles fill one round of 512 resident tiles with 5 partitions of 1664 keys
+    assert lib.dsp_paged_mq_partition_tokens(2, 12, 2, 128, 512, 8192) == 1664
+    assert lib.dsp_paged_mq_partition_tokens(4, 32, 8, 128, 512, 4096) == 4096  # 512 tiles
+    assert lib.dsp_paged_mq_partition_tokens(2, 16, 4, 64, 1024, 4096) == 1024  # 4 per CU
+    # short ones (verify) on 16-row tiles: ~2048 workgroups, partitions >= 128 keys
+    assert lib.dsp_paged_mq_partition_tokens(8, 16, 8, 128, 5, 2560) == 128
     assert lib.dsp_paged_decode_workspace_bytes(16, 32, 8, 128, 32768, 512) == 16 * 32 * 64 * 130 * 4
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, 512) == 0   # one partition
     # automatic split: room for the balanced split (B*KVH + waves slots of G rows) and for

@@ -82,7 +82,7 @@ def test_key_partitions_merge(hip, P):
 def test_auto_partition_single_long_chunk(hip):
     """One sequence, few tiles: the heuristic splits the keys (Qwen2.5-1.5B heads)."""
     from dispec_amd import _lib
-    assert _lib.lib().dsp_paged_mq_partition_tokens(1, 12, 2, 256, 3000) < 3000
+    assert _lib.lib().dsp_paged_mq_partition_tokens(1, 12, 2, 128, 256, 3000) < 3000
     out, ref = _run([256], [3000], 12, 2, 128, 340)
     assert_attention_close(out, ref, "auto partitions")
 
