@@ -526,6 +526,50 @@ def bench_c4(torch) -> dict:
     return res
 
 
+# ------------------------------------------------------------------------------ prefill
+def bench_prefill(torch) -> dict:
+    """Long query blocks over the paged cache (the 128-row prefill tile): Qwen3-4B heads
+    (Hq 32, KVH 8, D 128), blocks of 16 at random places.  `chunk`: 4 sequences whose last
+    512 of 4096 tokens are a prefill chunk; `fresh`: 2 sequences of 2048 tokens prefilled
+    at once.  FLOPs count the causal keys only (4 * Hq * D per query-key pair).  torch's
+    SDPA on contiguous K/V of the same shape is timed beside it for reference."""
+    from torch.nn.attention.bias import causal_lower_right
+
+    from dispec_amd.engine.hip_attn import paged_mq_attention
+    res = {}
+    dev = "cuda"
+    for name, B, q_len, ctx in (("chunk", 4, 512, 4096), ("fresh", 2, 2048, 2048)):
+        Hq, KVH, D, bs = 32, 8, 128, 16
+        nbs = ctx // bs
+        NB = B * nbs + 8
+        g = torch.Generator(device=dev).manual_seed(6001)
+        kc = torch.randn((NB * bs, KVH, D), generator=g, device=dev).to(torch.bfloat16)
+        vc = torch.randn((NB * bs, KVH, D), generator=g, device=dev).to(torch.bfloat16)
+        perm = torch.randperm(NB, generator=torch.Generator().manual_seed(6002))[:B * nbs]
+        bt = perm.view(B, nbs).to(torch.int32).to(dev)
+        q = torch.randn((B * q_len, Hq, D), generator=g, device=dev).to(torch.bfloat16)
+        cu = torch.arange(0, B + 1, dtype=torch.int32, device=dev) * q_len
+        ctx_t = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+        out = torch.empty_like(q)
+        fn = lambda: paged_mq_attention(q, kc, vc, bt, cu, ctx_t, Hq // KVH,  # noqa: E731
+                                        block_size=bs, max_q_len=q_len, max_ctx=ctx, out=out)
+        t = _time_gpu(torch, fn, 50, warmup=30)
+        keys = q_len * (ctx - q_len) + q_len * (q_len + 1) // 2
+        flops = 4 * B * Hq * D * keys
+        qq = q.view(B, q_len, Hq, D).transpose(1, 2).contiguous()
+        kk = torch.randn((B, Hq, ctx, D), generator=g, device=dev).to(torch.bfloat16)
+        vv = torch.randn_like(kk)
+        mask = causal_lower_right(q_len, ctx)
+        ts = _time_gpu(torch, lambda: torch.nn.functional.scaled_dot_product_attention(
+            qq, kk, vv, attn_mask=mask), 50, warmup=10)
+        res.update({f"prefill_{name}_us": t * 1e6, f"prefill_{name}_TFLOPs": flops / t / 1e12,
+                    f"prefill_{name}_mfma_frac": flops / t / 1e12 / PEAK_BF16_TFLOPS,
+                    f"prefill_{name}_torch_sdpa_contiguous_us": ts * 1e6})
+        del kc, vc, kk, vv
+        torch.cuda.empty_cache()
+    return res
+
+
 # ------------------------------------------------------------------------------ config 5
 def bench_c5(torch) -> dict:
     """Gather Qwen3-1.7B paged KV (28 L) of 8 requests x 4096 tokens into contiguous
@@ -654,7 +698,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-aux", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of c1,c2,c4,c5,skew,ceiling: run just these auxiliary configs and print "
+                    help="comma list of c1,c2,c4,c5,skew,ceiling,prefill: run just these auxiliary configs and print "
                          "their numbers (no headline line); 'copy' runs the 1 GiB plain "
                          "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters; "
                          "'graph' times a whole-model decode step, eager against HIP graph")
@@ -670,8 +714,8 @@ def main() -> int:
         return 2
     torch.cuda.set_device(0)
     configs = (("c1", bench_c1), ("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5),
-               ("skew", bench_skew), ("ceiling", bench_copy_ceiling), ("copy", bench_copy),
-               ("graph", bench_graph))
+               ("skew", bench_skew), ("ceiling", bench_copy_ceiling), ("prefill", bench_prefill),
+               ("copy", bench_copy), ("graph", bench_graph))
     if args.only:
         want = set(args.only.split(","))
         aux = {}
@@ -685,7 +729,7 @@ def main() -> int:
     dec = bench_decode(torch, args.steps, args.warmup)
     aux = {}
     if not args.no_aux:
-        for name, fn in configs[:6]:
+        for name, fn in configs[:7]:
             _log(f"config {name}")
             aux.update(fn(torch))
     cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)
