@@ -442,8 +442,9 @@ def bench_graph(torch) -> dict:
 def bench_c4(torch) -> dict:
     """Qwen3-1.7B shape (28 L, Hq 16, KVH 8, D 128): 32 sequences share a 2050-token
     prefix, fork it copy-on-write (the partial block is copied per sequence), append
-    suffixes ~U[64, 512], run a 5-query causal verify over the paged cache, then evict 10%
-    of the live blocks by copying them into a spill pool."""
+    suffixes ~U[64, 512], run a 5-query causal verify over the paged cache (with the shared
+    prompt blocks attended once for the batch, and per sequence for comparison), then evict
+    10% of the live blocks by copying them into a spill pool."""
     from dispec_amd.engine.hip_attn import paged_mq_attention
     from dispec_amd.kv.paged_cache import PagedKVCache
 
@@ -490,13 +491,19 @@ def bench_c4(torch) -> dict:
     out = torch.empty((L, S * K, Hq, D), dtype=torch.bfloat16, device=dev)
     max_ctx = bt.shape[1] * bs
 
-    def verify():
+    # the 128 full prompt blocks are shared by every fork: ModelRunner passes them as a
+    # shared prefix (2048 tokens), attended once for the batch; "plain" attends each
+    # sequence over its whole context
+    shared_tokens = (prefix // bs) * bs // 128 * 128
+
+    def verify(sp):
         for layer in range(L):
             paged_mq_attention(q[layer], cache.key[layer], cache.value[layer], bt, cu, ctx_t,
                                Hq // KVH, block_size=bs, max_q_len=K, max_ctx=max_ctx,
-                               out=out[layer])
+                               out=out[layer], shared_prefix_tokens=sp)
 
-    ver_s = _time_gpu(torch, verify, 10) / L
+    ver_s = _time_gpu(torch, lambda: verify(shared_tokens), 10) / L
+    plain_s = _time_gpu(torch, lambda: verify(0), 10) / L
     shared = (prefix // bs) * bs          # full prefix blocks, read by every sequence
     unique_tokens = shared + sum(c - shared for c in ctx)
     logical_tokens = sum(ctx)
@@ -515,6 +522,8 @@ def bench_c4(torch) -> dict:
         "c4_cow_pairs": len(pairs), "c4_cow_us": cow_s * 1e6, "c4_cow_GBps": cow_bytes / cow_s / 1e9,
         "c4_append_rows": n, "c4_append_GBps": 2 * 2 * n * cache.row_bytes / app_s / 1e9,
         "c4_verify_us_per_layer": ver_s * 1e6,
+        "c4_verify_shared_prefix_tokens": shared_tokens,
+        "c4_verify_plain_us_per_layer": plain_s * 1e6,
         "c4_verify_unique_GBps": unique_tokens * KVH * D * 4 / ver_s / 1e9,
         "c4_verify_logical_GBps": logical_tokens * KVH * D * 4 / ver_s / 1e9,
         "c4_verify_TFLOPs": flops / ver_s / 1e12,

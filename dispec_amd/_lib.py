@@ -51,6 +51,11 @@ SIGNATURES: dict[str, tuple] = {
                                        _P, c_int64, c_int32, _P, _P, c_int32, c_int32, c_int32,
                                        c_int32, c_float, c_int32, c_int32, c_int32, _P, c_size_t,
                                        _P, c_int64, c_int64, c_int32, _P, _P]),
+    "dsp_paged_mq_shared_prefix_partition_tokens": (c_int, [c_int32] * 7),
+    "dsp_paged_mq_attention_shared_prefix": (
+        c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64, _P, c_int64, c_int32,
+                _P, _P, c_int32, c_int32, c_int32, c_int32, c_float, c_int32, c_int32, c_int32,
+                c_int32, _P, c_size_t, _P, c_int64, c_int64, c_int32, _P, _P]),
     "dsp_kv_map_gemm": (c_int, [_P, _I64P, c_int32, c_int64, c_int64, _P, c_int64, _P, c_int64,
                                 c_int64, c_int64, c_int64, c_int32, c_int64, c_int64, _P, c_int32,
                                 c_int32, c_int32, c_int32, _P]),

@@ -46,8 +46,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
     int32_t G, float scale_log2, int32_t P, int32_t num_parts, int32_t tiles_max,
-    float* __restrict__ ws_acc, float* __restrict__ ws_ml, uint16_t* __restrict__ out,
-    int64_t ost, int64_t osh, int32_t* __restrict__ err_count) {
+    int32_t first_part, int32_t prefix_tokens, float* __restrict__ ws_acc,
+    float* __restrict__ ws_ml, uint16_t* __restrict__ out, int64_t ost, int64_t osh,
+    int32_t* __restrict__ err_count) {
   constexpr int NKK = D / 32;        // 32-dim K steps of the score MFMA
   constexpr int NT = D / 16;         // 16-dim output tiles
   constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
@@ -65,9 +66,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   auto s_acc = reinterpret_cast<float (*)[16][D + 1]>(s_raw);
   char* const slab_base = s_raw;
 
-  const int part = blockIdx.x % num_parts, tile = blockIdx.x / num_parts;
-  const int kvh = blockIdx.y, b = blockIdx.z;
+  // Partitions below first_part (a shared prefix, computed by the prefix pass of
+  // dsp_paged_mq_attention_shared_prefix) are not launched.
+  const int nsplit = num_parts - first_part;
   const int KVH = gridDim.y;
+  int xw = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int part = first_part + xw % nsplit, tile = xw / nsplit;
   const int q0 = kDecode ? b : cu_q[b];
   const int qlen = kDecode ? 1 : cu_q[b + 1] - q0;
   int ctx = ctx_lens[b];
@@ -80,9 +84,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
       if (threadIdx.x == 0 && part == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
       ctx = ctx < 0 ? 0 : max_ctx;
     }
-  } else if (ctx > max_ctx || ctx < qlen) {
+  } else if (ctx > max_ctx || ctx < qlen || ctx - qlen < prefix_tokens) {
     bad = true;
-    if (threadIdx.x == 0 && tile == 0 && part == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
+    if (threadIdx.x == 0 && tile == 0 && part == first_part && kvh == 0 && err_count)
+      atomicAdd(err_count, 1);
     ctx = 0;  // no keys: rows are written as zeros
   }
 
@@ -98,7 +103,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   const int kend = bad ? 0 : ctx - qlen + r_last / G + 1;  // keys any row of the tile sees
   // Split-K: this workgroup covers keys [kbeg, kfin) of the tile's causal range.
   const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
-  if (part >= nparts) return;
+  if (bad ? part != first_part : part >= nparts) return;  // a bad tile: one writer of zeros
   const int kbeg = part * P;
   const int kfin = min(kbeg + P, kend);
   const int64_t bt_row = int64_t(b) * bt_stride;
@@ -313,8 +318,8 @@ template <typename Tag, int D>
 __global__ __launch_bounds__(256) void mq_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
-    int32_t G, int32_t P, int32_t num_parts, int32_t tiles_max, uint16_t* __restrict__ out,
-    int64_t ost, int64_t osh) {
+    int32_t G, int32_t P, int32_t num_parts, int32_t tiles_max, int32_t prefix_tokens,
+    uint16_t* __restrict__ out, int64_t ost, int64_t osh) {
   constexpr int R = 256 / D;            // rows per workgroup
   constexpr int W = D < 64 ? D : 64;    // lanes that reduce one row's partition weights
   __shared__ float s_w[R][kMaxParts];
@@ -326,7 +331,8 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
   const int ctx = ctx_lens[b];
   const int rows = qlen * G;
   const int r0 = tile * 16;
-  if (qlen <= 0 || r0 >= rows || ctx > max_ctx || ctx < qlen) return;
+  if (qlen <= 0 || r0 >= rows || ctx > max_ctx || ctx < qlen || ctx - qlen < prefix_tokens)
+    return;
   const int r_last = min(r0 + 15, rows - 1);
   const int kend = ctx - qlen + r_last / G + 1;
   const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
@@ -412,13 +418,13 @@ int mq_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const u
     return launch_mq<Bf16Tag, true>(D, grid, s, q, q_stride_b, q_stride_h, k_cache, v_cache,
                                     num_slots, kv_stride_slot, kv_stride_head, block_table,
                                     bt_stride, log2_bs, no_cu, ctx_lens, max_ctx, G, scale_log2, P,
-                                    num_parts, int32_t(1), ws_acc, ws_ml, out, o_stride_b,
-                                    o_stride_h, err_count);
+                                    num_parts, int32_t(1), int32_t(0), int32_t(0), ws_acc, ws_ml,
+                                    out, o_stride_b, o_stride_h, err_count);
   return launch_mq<F16Tag, true>(D, grid, s, q, q_stride_b, q_stride_h, k_cache, v_cache,
                                  num_slots, kv_stride_slot, kv_stride_head, block_table, bt_stride,
                                  log2_bs, no_cu, ctx_lens, max_ctx, G, scale_log2, P, num_parts,
-                                 int32_t(1), ws_acc, ws_ml, out, o_stride_b, o_stride_h,
-                                 err_count);
+                                 int32_t(1), int32_t(0), int32_t(0), ws_acc, ws_ml, out,
+                                 o_stride_b, o_stride_h, err_count);
 }
 
 }  // namespace dsp_detail
@@ -472,21 +478,24 @@ extern "C" size_t dsp_paged_mq_workspace_bytes(int32_t B, int32_t Hq, int32_t KV
          sizeof(float);
 }
 
-extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
-                                      const void* k_cache, const void* v_cache,
-                                      int64_t num_slots, int64_t kv_stride_slot,
-                                      int64_t kv_stride_head, const int32_t* block_table,
-                                      int64_t bt_stride, int32_t block_size,
-                                      const int32_t* cu_q, const int32_t* ctx_lens, int32_t B,
-                                      int32_t Hq, int32_t KVH, int32_t D, float scale,
-                                      int32_t max_q_len, int32_t max_ctx,
-                                      int32_t partition_tokens, void* workspace,
-                                      size_t workspace_bytes, void* out, int64_t o_stride_t,
-                                      int64_t o_stride_h, int32_t dtype, int32_t* err_count,
-                                      dsp_stream_t stream) {
+namespace {
+
+// Both multi-query entry points.  prefix_tokens > 0: the first prefix_tokens keys are the
+// same physical blocks for every sequence and every query sees them (the caller's
+// precondition; a sequence with ctx - q_len < prefix_tokens is counted and zeroed); they
+// are attended once for the whole batch by the prefix pass, the rest per sequence.
+int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                      const void* k_cache, const void* v_cache, int64_t num_slots,
+                      int64_t kv_stride_slot, int64_t kv_stride_head, const int32_t* block_table,
+                      int64_t bt_stride, int32_t block_size, const int32_t* cu_q,
+                      const int32_t* ctx_lens, int32_t B, int32_t Hq, int32_t KVH, int32_t D,
+                      float scale, int32_t max_q_len, int32_t max_ctx, int32_t partition_tokens,
+                      void* workspace, size_t workspace_bytes, void* out, int64_t o_stride_t,
+                      int64_t o_stride_h, int32_t dtype, int32_t* err_count,
+                      dsp_stream_t stream, int32_t prefix_tokens) {
   DSP_HOST_CHECK(q && k_cache && v_cache && block_table && cu_q && ctx_lens && out, DSP_EINVAL);
   DSP_HOST_CHECK(B >= 0 && B <= 65535 && Hq > 0 && KVH > 0 && KVH <= 65535 && Hq % KVH == 0 &&
-                     max_q_len >= 0 && max_ctx >= 0 && num_slots >= 0,
+                     max_q_len >= 0 && max_ctx >= 0 && num_slots >= 0 && prefix_tokens >= 0,
                  DSP_EINVAL);
   DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16, DSP_EUNSUPPORTED);
   DSP_HOST_CHECK(D == 32 || D == 64 || D == 128, DSP_EUNSUPPORTED);
@@ -499,11 +508,19 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
                  DSP_EALIGN);
   const int G = Hq / KVH;
   const int64_t tiles = mq_tiles(max_q_len, G);
-  const int P = partition_tokens > 0
-                    ? partition_tokens
-                    : dsp_paged_mq_partition_tokens(B, Hq, KVH, D, max_q_len, max_ctx);
-  DSP_HOST_CHECK(P % 128 == 0, DSP_EINVAL);
+  int P = partition_tokens;
+  if (P <= 0)
+    P = prefix_tokens > 0 ? dsp_paged_mq_shared_prefix_partition_tokens(
+                                B, Hq, KVH, D, max_q_len, max_ctx, prefix_tokens)
+                          : dsp_paged_mq_partition_tokens(B, Hq, KVH, D, max_q_len, max_ctx);
+  DSP_HOST_CHECK(P > 0 && P % 128 == 0, DSP_EINVAL);
+  if (prefix_tokens > 0) {
+    DSP_HOST_CHECK(prefix_tokens % P == 0 && prefix_tokens < max_ctx, DSP_EINVAL);
+    DSP_HOST_CHECK(dsp_detail::shared_prefix_applies(D, block_size, B, num_slots, kv_stride_slot),
+                   DSP_EUNSUPPORTED);
+  }
   const int num_parts = max_ctx > 0 ? (max_ctx + P - 1) / P : 1;
+  const int first_part = prefix_tokens / P;
   DSP_HOST_CHECK(num_parts <= kMaxParts, DSP_EINVAL);
   DSP_HOST_CHECK(tiles * num_parts < (int64_t(1) << 31), DSP_EINVAL);
   const size_t need = dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, max_q_len, max_ctx, P);
@@ -511,8 +528,6 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
   DSP_HOST_CHECK(need == 0 || dsp_aligned(workspace, 16), DSP_EALIGN);
   float* ws_acc = static_cast<float*>(workspace);
   float* ws_ml = need ? ws_acc + int64_t(B) * KVH * tiles * num_parts * 16 * D : nullptr;
-  dim3 grid(static_cast<unsigned>(tiles * num_parts), static_cast<unsigned>(KVH),
-            static_cast<unsigned>(B));
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* qh = static_cast<const uint16_t*>(q);
@@ -521,30 +536,98 @@ extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t
   uint16_t* oh = static_cast<uint16_t*>(out);
   const int32_t lbs = dsp_log2i(block_size);
   const int32_t tm = static_cast<int32_t>(tiles);
-  int st;
-  if (dsp_detail::prefill_applies(D, block_size, int64_t(max_q_len) * G, num_slots,
-                                  kv_stride_slot))
+  const bool f16 = dtype == DSP_F16;
+  int st = DSP_OK;
+  if (prefix_tokens > 0)
+    st = dsp_detail::prefill_shared_prefix(qh, q_stride_t, q_stride_h, kh, vh, num_slots,
+                                           kv_stride_slot, kv_stride_head, block_table, lbs, cu_q,
+                                           B, KVH, G, D, scale_log2, max_q_len, max_ctx, P,
+                                           num_parts, tm, prefix_tokens, ws_acc, ws_ml, f16, s);
+  if (st != DSP_OK) return st;
+  if (prefix_tokens == 0 && dsp_detail::prefill_applies(D, block_size, int64_t(max_q_len) * G,
+                                                         num_slots, kv_stride_slot)) {
     st = dsp_detail::prefill_attention(qh, q_stride_t, q_stride_h, kh, vh, num_slots,
                                        kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs,
                                        cu_q, ctx_lens, B, KVH, G, D, scale_log2, max_q_len, max_ctx,
                                        P, num_parts, tm, ws_acc, ws_ml, oh, o_stride_t, o_stride_h,
-                                       dtype == DSP_F16, err_count, s);
-  else if (dtype == DSP_BF16)
-    st = launch_mq<Bf16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
-                            kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
-                            ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, ws_acc, ws_ml,
-                            oh, o_stride_t, o_stride_h, err_count);
-  else
-    st = launch_mq<F16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
-                           kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
-                           ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, ws_acc, ws_ml, oh,
-                           o_stride_t, o_stride_h, err_count);
+                                       f16, err_count, s);
+  } else {
+    dim3 grid(static_cast<unsigned>(tiles * (num_parts - first_part)), static_cast<unsigned>(KVH),
+              static_cast<unsigned>(B));
+    if (!f16)
+      st = launch_mq<Bf16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
+                              kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
+                              ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, first_part,
+                              prefix_tokens, ws_acc, ws_ml, oh, o_stride_t, o_stride_h, err_count);
+    else
+      st = launch_mq<F16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
+                             kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
+                             ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, first_part,
+                             prefix_tokens, ws_acc, ws_ml, oh, o_stride_t, o_stride_h, err_count);
+  }
   if (st != DSP_OK || num_parts <= 1) return st;
   dim3 cgrid(static_cast<unsigned>(tiles * 16 / (256 / D)), static_cast<unsigned>(KVH),
              static_cast<unsigned>(B));
-  if (dtype == DSP_BF16)
+  if (!f16)
     return launch_mq_combine<Bf16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
-                                      num_parts, tm, oh, o_stride_t, o_stride_h);
+                                      num_parts, tm, prefix_tokens, oh, o_stride_t, o_stride_h);
   return launch_mq_combine<F16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
-                                   num_parts, tm, oh, o_stride_t, o_stride_h);
+                                   num_parts, tm, prefix_tokens, oh, o_stride_t, o_stride_h);
+}
+
+}  // namespace
+
+extern "C" int dsp_paged_mq_shared_prefix_partition_tokens(int32_t B, int32_t Hq, int32_t KVH,
+                                                           int32_t D, int32_t max_q_len,
+                                                           int32_t max_ctx,
+                                                           int32_t prefix_tokens) {
+  (void)D;
+  (void)max_ctx;
+  if (B <= 0 || KVH <= 0 || Hq % KVH != 0 || max_q_len <= 0 || prefix_tokens <= 0 ||
+      prefix_tokens % 128 != 0)
+    return 128;
+  // The prefix pass runs B * max_q_len * G rows per KV head in 128-row tiles: split the
+  // prefix until it has a workgroup for every other CU, in partitions that divide it (more,
+  // shorter partitions cost more in fixed per-workgroup latency and merge traffic than
+  // they gain; config 4: 256-key partitions 38 us, 128-key 43 us).
+  const int64_t tiles = dsp_detail::prefill_tiles(int32_t(int64_t(B) * max_q_len), Hq / KVH);
+  const int64_t want = int64_t(dsp_detail::device_cus()) / 2;
+  for (int p = 512; p > 128; p -= 128)
+    if (prefix_tokens % p == 0 && tiles * KVH * (prefix_tokens / p) >= want) return p;
+  return 128;
+}
+
+extern "C" int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                      const void* k_cache, const void* v_cache,
+                                      int64_t num_slots, int64_t kv_stride_slot,
+                                      int64_t kv_stride_head, const int32_t* block_table,
+                                      int64_t bt_stride, int32_t block_size,
+                                      const int32_t* cu_q, const int32_t* ctx_lens, int32_t B,
+                                      int32_t Hq, int32_t KVH, int32_t D, float scale,
+                                      int32_t max_q_len, int32_t max_ctx,
+                                      int32_t partition_tokens, void* workspace,
+                                      size_t workspace_bytes, void* out, int64_t o_stride_t,
+                                      int64_t o_stride_h, int32_t dtype, int32_t* err_count,
+                                      dsp_stream_t stream) {
+  return mq_attention_impl(q, q_stride_t, q_stride_h, k_cache, v_cache, num_slots,
+                           kv_stride_slot, kv_stride_head, block_table, bt_stride, block_size,
+                           cu_q, ctx_lens, B, Hq, KVH, D, scale, max_q_len, max_ctx,
+                           partition_tokens, workspace, workspace_bytes, out, o_stride_t,
+                           o_stride_h, dtype, err_count, stream, 0);
+}
+
+extern "C" int dsp_paged_mq_attention_shared_prefix(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+    const void* v_cache, int64_t num_slots, int64_t kv_stride_slot, int64_t kv_stride_head,
+    const int32_t* block_table, int64_t bt_stride, int32_t block_size, const int32_t* cu_q,
+    const int32_t* ctx_lens, int32_t B, int32_t Hq, int32_t KVH, int32_t D, float scale,
+    int32_t max_q_len, int32_t max_ctx, int32_t prefix_tokens, int32_t partition_tokens,
+    void* workspace, size_t workspace_bytes, void* out, int64_t o_stride_t, int64_t o_stride_h,
+    int32_t dtype, int32_t* err_count, dsp_stream_t stream) {
+  DSP_HOST_CHECK(prefix_tokens > 0 && prefix_tokens % 128 == 0, DSP_EINVAL);
+  return mq_attention_impl(q, q_stride_t, q_stride_h, k_cache, v_cache, num_slots,
+                           kv_stride_slot, kv_stride_head, block_table, bt_stride, block_size,
+                           cu_q, ctx_lens, B, Hq, KVH, D, scale, max_q_len, max_ctx,
+                           partition_tokens, workspace, workspace_bytes, out, o_stride_t,
+                           o_stride_h, dtype, err_count, stream, prefix_tokens);
 }

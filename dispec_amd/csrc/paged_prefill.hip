@@ -39,6 +39,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int kWaves = 4, kThreads = 64 * kWaves;
 constexpr int kRows = 32 * kWaves;  // packed rows per workgroup
 constexpr int kChunk = 64;          // keys per LDS chunk
+constexpr int kMaxSharedSeqs = 1024;  // sequences of a shared-prefix launch (cu_q in LDS)
 
 template <typename Tag>
 __device__ __forceinline__ f32x16 mfma32x32(dsp_u32x4 a, dsp_u32x4 b, f32x16 c) {
@@ -69,7 +70,13 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 
-template <typename Tag, int D>
+// kShared: the prefix pass of a shared-prefix (cascade) launch.  Packed row r is token
+// r / G of the whole batch (every sequence's queries), query head kvh*G + r % G; the keys
+// are the first prefix_tokens of block-table row 0, which every sequence shares and every
+// query sees whole (no mask).  Partition `part` covers keys [part*P, part*P + P) and is
+// written, for every row, to that row's own (sequence, 16-row tile) slot of the merge
+// layout; the sequences' suffix partitions follow it.
+template <typename Tag, int D, bool kShared>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t qst, int64_t qsh, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
@@ -77,7 +84,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
     int32_t G, float scale_log2, int32_t P, int32_t num_parts, int32_t tiles16_max,
     float* __restrict__ ws_acc, float* __restrict__ ws_ml, uint16_t* __restrict__ out,
-    int64_t ost, int64_t osh, int32_t* __restrict__ err_count) {
+    int64_t ost, int64_t osh, int32_t* __restrict__ err_count, int32_t nseq,
+    int32_t prefix_tokens, int32_t ws_parts) {
   constexpr int NKS = D / 16;        // 16-dim steps of the score MFMA
   constexpr int NDT = D / 32;        // 32-dim output tiles
   constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
@@ -87,6 +95,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   constexpr int LPW = SLAB / 1024 / kWaves;      // DMA loads per wave per slab
   static_assert(LPW >= 1, "every wave loads part of a chunk");
   __shared__ __attribute__((aligned(1024))) char lds[2][2][SLAB];  // [buffer][K | V]
+  __shared__ int32_t s_cu[kShared ? kMaxSharedSeqs + 1 : 1];         // cu_q, prefix pass
 
   // XCD-aware order: the dispatcher hands workgroup `lin` to XCD lin % 8.  Each XCD gets a
   // contiguous range of logical ids, so the tiles of one (sequence, KV head) -- which read
@@ -101,23 +110,38 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int kvh = int((lg / X) % KVH), b = int(lg / X / KVH);
   const int ntiles = X / num_parts;
   const int part = xl % num_parts, tile = ntiles - 1 - xl / num_parts;
-  const int q0 = cu_q[b], qlen = cu_q[b + 1] - q0;
-  const int ctx = ctx_lens[b];
+  int q0, qlen, ctx, kend;
+  if constexpr (kShared) {
+    // all tokens of the batch; the causal limit never binds (ctx - qlen + qi >= max_ctx)
+    q0 = 0;
+    qlen = cu_q[nseq];
+    ctx = qlen + max_ctx;
+    kend = prefix_tokens;
+    // staged for the epilogue's row -> sequence search (published by the first chunk's
+    // barrier: every workgroup that gets past the checks below runs at least one chunk)
+    for (int i = threadIdx.x; i <= nseq; i += kThreads) s_cu[i] = cu_q[i];
+  } else {
+    q0 = cu_q[b];
+    qlen = cu_q[b + 1] - q0;
+    ctx = ctx_lens[b];
+  }
   const int rows = qlen * G;
   const int r0 = tile * kRows;
   if (qlen <= 0 || r0 >= rows) return;
-  if (ctx > max_ctx || ctx < qlen) {  // bad lengths: counted once, the rows are zeros
-    if (part != 0) return;
-    if (threadIdx.x == 0 && tile == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
-    for (int i = threadIdx.x; i < kRows * D; i += kThreads) {
-      const int rr = r0 + i / D;
-      if (rr < rows)
-        out[int64_t(q0 + rr / G) * ost + int64_t(kvh * G + rr % G) * osh + i % D] = 0;
+  if constexpr (!kShared) {
+    if (ctx > max_ctx || ctx < qlen) {  // bad lengths: counted once, the rows are zeros
+      if (part != 0) return;
+      if (threadIdx.x == 0 && tile == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
+      for (int i = threadIdx.x; i < kRows * D; i += kThreads) {
+        const int rr = r0 + i / D;
+        if (rr < rows)
+          out[int64_t(q0 + rr / G) * ost + int64_t(kvh * G + rr % G) * osh + i % D] = 0;
+      }
+      return;
     }
-    return;
+    const int r_last = min(r0 + kRows - 1, rows - 1);
+    kend = ctx - qlen + r_last / G + 1;  // keys any row of the tile sees
   }
-  const int r_last = min(r0 + kRows - 1, rows - 1);
-  const int kend = ctx - qlen + r_last / G + 1;  // keys any row of the tile sees
   const int kbeg = part * P;
   if (kbeg >= kend) return;
   const int kfin = min(kbeg + P, kend);
@@ -302,23 +326,35 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   // 8*(j/4) + 4*hl + j%4]
   lpart += dsp_shfl_xor(lpart, 32);
   if (!row_ok) return;
-  const int st = r / 16, rr = r % 16;                    // 16-row tile of the merge layout
-  if (st >= tiles16_max) return;  // q_len past the caller's max_q_len: rows not covered
-  const int r_last16 = min(st * 16 + 15, rows - 1);
-  const int kend16 = ctx - qlen + r_last16 / G + 1;
-  const int nparts16 = (kend16 + P - 1) / P;
-  if (part >= nparts16) return;  // the merge for this 16-row tile does not read this partition
-  if (nparts16 == 1) {
-    const float inv = lpart > 0.f ? 1.f / lpart : 0.f;
-    uint16_t* o = out + int64_t(q0 + qi) * ost + int64_t(h) * osh;
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        o[32 * dt + 8 * (j >> 2) + 4 * hl + (j & 3)] = narrow<Tag>(acc[dt][j] * inv);
-    return;
+  int sb = b, lr = r;  // the row's sequence and its packed row there
+  if constexpr (kShared) {
+    int lo = 0, hi = nseq - 1;  // last sequence whose first token is <= qi
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_cu[mid] <= qi) lo = mid; else hi = mid - 1;
+    }
+    sb = lo;
+    lr = (qi - s_cu[lo]) * G + (r % G);
   }
-  const int64_t slot = ((int64_t(b) * KVH + kvh) * tiles16_max + st) * num_parts + part;
+  const int st = lr / 16, rr = lr % 16;                  // 16-row tile of the merge layout
+  if (st >= tiles16_max) return;  // q_len past the caller's max_q_len: rows not covered
+  if constexpr (!kShared) {
+    const int r_last16 = min(st * 16 + 15, rows - 1);
+    const int kend16 = ctx - qlen + r_last16 / G + 1;
+    const int nparts16 = (kend16 + P - 1) / P;
+    if (part >= nparts16) return;  // the merge for this 16-row tile does not read it
+    if (nparts16 == 1) {
+      const float inv = lpart > 0.f ? 1.f / lpart : 0.f;
+      uint16_t* o = out + int64_t(q0 + qi) * ost + int64_t(h) * osh;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          o[32 * dt + 8 * (j >> 2) + 4 * hl + (j & 3)] = narrow<Tag>(acc[dt][j] * inv);
+      return;
+    }
+  }
+  const int64_t slot = ((int64_t(sb) * KVH + kvh) * tiles16_max + st) * ws_parts + part;
   float* a = ws_acc + (slot * 16 + rr) * D;
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
@@ -330,6 +366,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     ws_ml[2 * (slot * 16 + rr)] = m;
     ws_ml[2 * (slot * 16 + rr) + 1] = lpart;
   }
+}
+
+template <bool kShared, typename... A>
+int launch_prefill(int D, bool f16, dim3 grid, hipStream_t s, A... args) {
+  if (D == 128) {
+    if (f16) paged_prefill_kernel<F16Tag, 128, kShared><<<grid, kThreads, 0, s>>>(args...);
+    else paged_prefill_kernel<Bf16Tag, 128, kShared><<<grid, kThreads, 0, s>>>(args...);
+  } else {
+    if (f16) paged_prefill_kernel<F16Tag, 64, kShared><<<grid, kThreads, 0, s>>>(args...);
+    else paged_prefill_kernel<Bf16Tag, 64, kShared><<<grid, kThreads, 0, s>>>(args...);
+  }
+  return dsp_launch_status();
 }
 
 }  // namespace
@@ -358,19 +406,37 @@ int prefill_attention(const uint16_t* q, int64_t q_stride_t, int64_t q_stride_h,
   const int64_t tiles = prefill_tiles(max_q_len, G);
   dim3 grid(static_cast<unsigned>(tiles * num_parts), static_cast<unsigned>(KVH),
             static_cast<unsigned>(B));
-#define DSP_PREFILL_ARGS                                                                     \
-  q, q_stride_t, q_stride_h, k_cache, v_cache, num_slots, kv_stride_slot, kv_stride_head,    \
-      block_table, bt_stride, log2_bs, cu_q, ctx_lens, max_ctx, G, scale_log2, P, num_parts, \
-      tiles16_max, ws_acc, ws_ml, out, o_stride_t, o_stride_h, err_count
-  if (D == 128) {
-    if (f16) paged_prefill_kernel<F16Tag, 128><<<grid, kThreads, 0, s>>>(DSP_PREFILL_ARGS);
-    else paged_prefill_kernel<Bf16Tag, 128><<<grid, kThreads, 0, s>>>(DSP_PREFILL_ARGS);
-  } else {
-    if (f16) paged_prefill_kernel<F16Tag, 64><<<grid, kThreads, 0, s>>>(DSP_PREFILL_ARGS);
-    else paged_prefill_kernel<Bf16Tag, 64><<<grid, kThreads, 0, s>>>(DSP_PREFILL_ARGS);
-  }
-#undef DSP_PREFILL_ARGS
-  return dsp_launch_status();
+  return launch_prefill<false>(D, f16, grid, s, q, q_stride_t, q_stride_h, k_cache, v_cache,
+                               num_slots, kv_stride_slot, kv_stride_head, block_table, bt_stride,
+                               log2_bs, cu_q, ctx_lens, max_ctx, G, scale_log2, P, num_parts,
+                               tiles16_max, ws_acc, ws_ml, out, o_stride_t, o_stride_h,
+                               err_count, B, int32_t(0), num_parts);
+}
+
+int prefill_shared_prefix(const uint16_t* q, int64_t q_stride_t, int64_t q_stride_h,
+                          const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,
+                          int64_t kv_stride_slot, int64_t kv_stride_head,
+                          const int32_t* block_table, int32_t log2_bs, const int32_t* cu_q,
+                          int32_t B, int32_t KVH, int32_t G, int32_t D, float scale_log2,
+                          int32_t max_q_len, int32_t max_ctx, int32_t P, int32_t num_parts,
+                          int32_t tiles16_max, int32_t prefix_tokens, float* ws_acc,
+                          float* ws_ml, bool f16, hipStream_t s) {
+  const int64_t tiles = (int64_t(B) * max_q_len * G + kRows - 1) / kRows;
+  const int32_t prefix_parts = prefix_tokens / P;
+  dim3 grid(static_cast<unsigned>(tiles * prefix_parts), static_cast<unsigned>(KVH), 1u);
+  int32_t* no_err = nullptr;
+  uint16_t* no_out = nullptr;
+  return launch_prefill<true>(D, f16, grid, s, q, q_stride_t, q_stride_h, k_cache, v_cache,
+                              num_slots, kv_stride_slot, kv_stride_head, block_table, int64_t(0),
+                              log2_bs, cu_q, cu_q, max_ctx, G, scale_log2, P, prefix_parts,
+                              tiles16_max, ws_acc, ws_ml, no_out, int64_t(0), int64_t(0), no_err,
+                              B, prefix_tokens, num_parts);
+}
+
+bool shared_prefix_applies(int32_t D, int32_t block_size, int32_t B, int64_t num_slots,
+                           int64_t kv_stride_slot) {
+  return (D == 64 || D == 128) && block_size >= 16 && B >= 1 && B <= kMaxSharedSeqs &&
+         num_slots >= 16 && kv_stride_slot < (int64_t(1) << 25);
 }
 
 }  // namespace dsp_detail

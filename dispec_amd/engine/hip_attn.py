@@ -118,7 +118,7 @@ def decode_workspace(batch, num_heads, num_kv_heads, head_dim, max_ctx, device):
 
 def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_groups,
                        block_size=16, scale=None, max_q_len=None, max_ctx=None, out=None,
-                       err=None, partition_tokens=0, workspace=None):
+                       err=None, partition_tokens=0, workspace=None, shared_prefix_tokens=0):
     """Multi-query paged attention: speculative verify, chunked and fresh prefill.
 
     Per sequence b, rows q[cu_q[b]:cu_q[b+1]] are the last q_len_b tokens of a ctx_b-token
@@ -132,6 +132,10 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
                  which costs a device->host copy)
     partition_tokens: split-K key partition (0: chosen from the shape); workspace: an
                  optional preallocated fp32 buffer for the partial results
+    shared_prefix_tokens: > 0 when the first that many context tokens of every sequence
+                 are the same physical blocks (copy-on-write forks, prefix-cache hits) and
+                 every query sees them all: they are attended once for the whole batch
+                 (a multiple of 128, < max_ctx; dsp_paged_mq_attention_shared_prefix)
     returns:     (sum q_len, num_heads, head_dim) in q's dtype
     """
     _lib.require_gpu(q, k_cache, v_cache, block_table, cu_q, ctx_lens)
@@ -164,17 +168,26 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
         raise ValueError("out must have q's shape and dtype with head_dim contiguous")
     L = _lib.lib()
-    P = partition_tokens or L.dsp_paged_mq_partition_tokens(B, Hq, KVH, D, int(max_q_len),
-                                                            int(max_ctx))
+    sp = int(shared_prefix_tokens)
+    if sp:
+        P = partition_tokens or L.dsp_paged_mq_shared_prefix_partition_tokens(
+            B, Hq, KVH, D, int(max_q_len), int(max_ctx), sp)
+    else:
+        P = partition_tokens or L.dsp_paged_mq_partition_tokens(B, Hq, KVH, D, int(max_q_len),
+                                                                int(max_ctx))
     need = L.dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, int(max_q_len), int(max_ctx), P)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    _lib.check(L.dsp_paged_mq_attention(
-        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), S,
-        k_cache.stride(0), k_cache.stride(1), block_table.data_ptr(), block_table.stride(0),
-        block_size, cu_q.data_ptr(), ctx_lens.data_ptr(), B, Hq, KVH, D, float(scale),
-        int(max_q_len), int(max_ctx), int(P), _lib.ptr(workspace), ws_bytes, out.data_ptr(),
-        out.stride(0), out.stride(1), _lib.dtype_code(q.dtype), _lib.ptr(err),
-        _lib.stream_of(q)), "dsp_paged_mq_attention")
+    head = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), S,
+            k_cache.stride(0), k_cache.stride(1), block_table.data_ptr(), block_table.stride(0),
+            block_size, cu_q.data_ptr(), ctx_lens.data_ptr(), B, Hq, KVH, D, float(scale),
+            int(max_q_len), int(max_ctx))
+    tail = (_lib.ptr(workspace), ws_bytes, out.data_ptr(), out.stride(0), out.stride(1),
+            _lib.dtype_code(q.dtype), _lib.ptr(err), _lib.stream_of(q))
+    if sp:
+        _lib.check(L.dsp_paged_mq_attention_shared_prefix(*head, sp, int(P), *tail),
+                   "dsp_paged_mq_attention_shared_prefix")
+    else:
+        _lib.check(L.dsp_paged_mq_attention(*head, int(P), *tail), "dsp_paged_mq_attention")
     return out

@@ -13,7 +13,11 @@ the HF modules, unchanged.  What the backend replaces is the KV path inside `_at
                                         per-token slot table and no per-sequence loop)
   * anything else (fresh or chunked   -> dsp_paged_mq_attention, one launch for the whole
     prefill, speculative verify,        ragged batch with the bottom-right causal mask
-    mixed decode + prefill)             (the reference loops over sequences with SDPA)
+    mixed decode + prefill)             (the reference loops over sequences with SDPA);
+                                        when the sequences' tables start with the same
+                                        blocks (copy-on-write forks of one prompt,
+                                        prefix-cache hits) the shared-prefix variant
+                                        attends those blocks once for the whole batch
 
 Only "hip" is accepted: the reference's "native"/"triton" backends are torch/Triton
 code paths this package does not carry.
@@ -53,6 +57,7 @@ class _Batch:
     max_ctx: int
     decode: bool
     workspace: torch.Tensor | None = None
+    shared_prefix: int = 0   # leading context tokens all sequences share (0: none used)
 
 
 class ModelRunner:
@@ -83,6 +88,10 @@ class ModelRunner:
         self.rotary_emb = core.rotary_emb
         self._rope_dummy = torch.zeros(1, 1, device=self.device, dtype=self.dtype)
         self.fused = self._build_fused() if fuse else False
+        # shared-prefix attention: used when at least this many sequences share at least
+        # this many leading tokens (fewer gain nothing over per-sequence attention)
+        self.shared_prefix_min_seqs = 4
+        self.shared_prefix_min_tokens = 512
 
     def _build_fused(self) -> bool:
         """One GEMM for q/k/v and one for gate/up per layer (model_runner.py:93-118)."""
@@ -125,10 +134,28 @@ class ModelRunner:
                 host[2 * B + 1 + i * width: 2 * B + 1 + i * width + len(m.block_ids)] = \
                     torch.tensor(m.block_ids, dtype=torch.int32)
         dev = host.to(cache.key.device)                 # one H2D copy for all metadata
+        decode = all(m.q_len == 1 for m in seq_meta)
+        shared = 0 if decode else self._shared_prefix(seq_meta, host[2 * B + 1:].view(B, width),
+                                                      cache.block_size)
         return _Batch(block_table=dev[2 * B + 1:].view(B, width), ctx_lens=dev[:B],
                       cu_q=dev[B:2 * B + 1], max_q_len=max(m.q_len for m in seq_meta),
-                      max_ctx=width * cache.block_size,
-                      decode=all(m.q_len == 1 for m in seq_meta))
+                      max_ctx=width * cache.block_size, decode=decode, shared_prefix=shared)
+
+    def _shared_prefix(self, seq_meta: list[SeqMeta], table: torch.Tensor, bs: int) -> int:
+        """Leading context tokens whose blocks every sequence's table shares and every query
+        sees, rounded down to a multiple of 128 -- or 0 when the batch is too small, the
+        prefix too short, or the shape one the shared-prefix kernels do not serve."""
+        B = len(seq_meta)
+        if (B < self.shared_prefix_min_seqs or B > 1024 or bs < 16
+                or self.head_dim not in (64, 128)):
+            return 0
+        limit = min(m.ctx_len - m.q_len for m in seq_meta) // bs   # full blocks all queries see
+        if limit * bs < self.shared_prefix_min_tokens:
+            return 0
+        same = (table[:, :limit] == table[0, :limit]).all(0)
+        n = limit if bool(same.all()) else int(torch.argmin(same.to(torch.int8)))
+        tokens = n * bs // 128 * 128
+        return tokens if tokens >= self.shared_prefix_min_tokens else 0
 
     # -- attention for one layer --------------------------------------------------------
     def _attention(self, layer, x, cos, sin, write_slots, cache, layer_idx, batch: _Batch):
@@ -157,7 +184,8 @@ class ModelRunner:
             o = paged_mq_attention(
                 q, cache.key[layer_idx], cache.value[layer_idx], batch.block_table, batch.cu_q,
                 batch.ctx_lens, self.kv_groups, block_size=cache.block_size, scale=self.scale,
-                max_q_len=batch.max_q_len, max_ctx=batch.max_ctx)
+                max_q_len=batch.max_q_len, max_ctx=batch.max_ctx,
+                shared_prefix_tokens=batch.shared_prefix)
         return attn.o_proj(o.reshape(T, self.num_heads * self.head_dim))
 
     @torch.inference_mode()

@@ -205,6 +205,31 @@ int dsp_paged_mq_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h
                            int64_t o_stride_h, int32_t dtype, int32_t* err_count,
                            dsp_stream_t stream);
 
+/* J4, shared prefix (cascade).  The same attention when the first prefix_tokens context
+ * tokens of every sequence are the same physical blocks -- copy-on-write forks of one
+ * prompt (BlockManager.fork, dispec/kv/block_manager.py:119-126) or prefix-cache hits
+ * (PrefixCache.match, dispec/kv/prefix_cache.py:39-50) -- and every query sees all of
+ * them (prefix_tokens <= ctx_b - q_len_b; a sequence breaking this is counted in
+ * err_count and zeroed).  The prefix keys are read once for every query row of the batch
+ * (block-table row 0 supplies them) instead of once per sequence; the suffixes run per
+ * sequence; one merge folds both.  No reference counterpart: the reference attends each
+ * sequence over its whole context (model_runner.py:160-185); the result is the same
+ * function.  prefix_tokens: a multiple of 128 and of partition_tokens, < max_ctx;
+ * partition_tokens 0 = dsp_paged_mq_shared_prefix_partition_tokens.  D 64 or 128, blocks
+ * of >= 16 tokens, B <= 1024 (else DSP_EUNSUPPORTED).  The workspace is
+ * dsp_paged_mq_workspace_bytes at the partition used (always needed). */
+int dsp_paged_mq_shared_prefix_partition_tokens(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
+                                                int32_t max_q_len, int32_t max_ctx,
+                                                int32_t prefix_tokens);
+int dsp_paged_mq_attention_shared_prefix(
+    const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+    const void* v_cache, int64_t num_slots, int64_t kv_stride_slot, int64_t kv_stride_head,
+    const int32_t* block_table, int64_t bt_stride, int32_t block_size, const int32_t* cu_q,
+    const int32_t* ctx_lens, int32_t B, int32_t Hq, int32_t KVH, int32_t D, float scale,
+    int32_t max_q_len, int32_t max_ctx, int32_t prefix_tokens, int32_t partition_tokens,
+    void* workspace, size_t workspace_bytes, void* out, int64_t o_stride_t, int64_t o_stride_h,
+    int32_t dtype, int32_t* err_count, dsp_stream_t stream);
+
 /* ------------------------------------------------------------------------------ J5b
  * The cross-model map GEMM: C[M, N] = epilogue(A[M, K] . Bt[N, K]^T), bf16 operands,
  * fp32 accumulation (MFMA).  Replaces the matmuls of LayerMap.apply

@@ -117,6 +117,28 @@ def test_batched_decode_many_sequences():
         cur = [c + 1 for c in cur]
 
 
+def test_verify_of_forked_sequences_uses_the_shared_prefix():
+    """Speculative verify after copy-on-write forks of one 640-token prompt (40 shared
+    blocks, block_manager.py:119-126): the runner finds the shared blocks and attends them
+    once for the batch (dsp_paged_mq_attention_shared_prefix); logits match the native
+    path sequence by sequence."""
+    from dispec_amd.engine.model_runner import SeqMeta
+    gm, cm = _pair("qwen3")
+    both = _Both(gm, cm, num_blocks=96)
+    g = torch.Generator().manual_seed(12)
+    prompt = torch.randint(0, 128, (640,), generator=g).tolist()
+    both.forward([(0, prompt, 0)])
+    for child in range(1, 5):
+        _, copies = both.cache.manager.cow_fork(0, child)
+        assert copies == []                      # block-aligned prompt: every block shared
+    drafts = [torch.randint(0, 128, (5,), generator=g).tolist() for _ in range(5)]
+    got, ref = both.forward([(sid, drafts[sid], 640) for sid in range(5)])
+    assert _cos(got, ref).min() >= 0.999
+    mgr = both.cache.manager
+    meta = [SeqMeta(list(mgr.block_table(s).block_ids), 5, 645) for s in range(5)]
+    assert both.runner._batch(meta, both.cache).shared_prefix == 640
+
+
 def test_rejects_other_backends():
     from dispec_amd.engine.model_runner import ModelRunner
     with pytest.raises(ValueError, match="hip"):
