@@ -209,7 +209,35 @@ def bench_cpu_baseline(torch) -> dict:
                 cores=torch.get_num_threads(), kind="port",
                 sample=f"config 3, 1 layer, {nseq} of {B} sequences x {ctx} tokens, median of "
                        f"{len(times) - 1} after 1 warmup, scaled x{B // nseq}",
-                cpu_model=_cpu_model())
+                cpu_model=_cpu_model(), transport=_xfer_reference(torch))
+
+
+def _xfer_reference(torch) -> dict:
+    """The reference's TCP handoff (torch.save pickle of CPU copies, bytearray receive,
+    torch.load, .to(device): dispec/transport/tcp.py:19-36, 61-70) on the same payload and
+    loopback connection as bench_xfer, with the same export and import kernels."""
+    import threading
+
+    from oracle import ref_torch
+    x = _xfer_setup(torch)
+
+    def step():
+        k, v = x["src"].export_contiguous(x["src_ids"], len(x["tokens"]))
+        th = threading.Thread(target=ref_torch.tcp_send_pickle,
+                              args=(x["a"], x["tokens"], k, v, {"request_id": 1}))
+        th.start()
+        _, k2, v2, _ = ref_torch.tcp_recv_pickle(x["b"], "cuda")
+        th.join()
+        x["dst"].import_contiguous(x["dst_ids"], k2, v2)
+
+    t = _xfer_time(torch, step, iters=2)
+    x["a"].close()
+    x["b"].close()
+    res = {"GBps": round(x["payload_bytes"] / t / 1e9, 3), "ms": round(t * 1e3, 1),
+           "sample": "one 4096-token, 28-layer payload (470 MB), loopback TCP, median of 2"}
+    del x
+    torch.cuda.empty_cache()
+    return res
 
 
 def _cpu_model() -> str:
@@ -579,6 +607,81 @@ def bench_prefill(torch) -> dict:
     return res
 
 
+# ------------------------------------------------------------------------------ transport
+def _xfer_setup(torch):
+    """One escalation payload of config 5's source model (Qwen3-1.7B: 28 layers, 8 KV heads,
+    head_dim 128) for a 4096-token request, exported from a pool with random block
+    placement, and a second pool to import it into; a loopback TCP connection."""
+    import socket
+
+    from dispec_amd.kv.paged_cache import PagedKVCache
+    L, KVH, D, bs, T = 28, 8, 128, 16, 4096
+    dev = "cuda"
+    nb = T // bs
+    src = PagedKVCache(L, nb + 8, bs, KVH, D, device=dev)
+    dst = PagedKVCache(L, nb + 8, bs, KVH, D, device=dev)
+    _fill_randn(torch, src.key, 5101)
+    _fill_randn(torch, src.value, 5102)
+    g = torch.Generator().manual_seed(5103)
+    src_ids = torch.randperm(nb + 8, generator=g)[:nb].tolist()
+    dst_ids = torch.randperm(nb + 8, generator=g)[:nb].tolist()
+    tokens = torch.randint(0, 150_000, (T,), generator=g).tolist()
+    srv = socket.socket(socket.AF_INET, socket.SOCK_STREAM)
+    srv.bind(("127.0.0.1", 0))
+    srv.listen(1)
+    a = socket.create_connection(srv.getsockname())
+    b, _ = srv.accept()
+    srv.close()
+    for s in (a, b):
+        s.setsockopt(socket.IPPROTO_TCP, socket.TCP_NODELAY, 1)
+    return dict(src=src, dst=dst, src_ids=src_ids, dst_ids=dst_ids, tokens=tokens, a=a, b=b,
+                payload_bytes=2 * L * T * KVH * D * 2)
+
+
+def _xfer_time(torch, step, iters=4) -> float:
+    step()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(iters):
+        t = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t)
+    return statistics.median(times)
+
+
+def bench_xfer(torch) -> dict:
+    """Escalation handoff over TCP (§8(f) 3): export (J5a gather) -> TcpTransport.send ->
+    loopback socket -> TcpTransport.recv into GPU memory -> import (J5c scatter), sender
+    and receiver in two threads of this process.  GB/s = K + V payload bytes / wall time
+    of one handoff; the reference's pickle framing is timed in the CPU-baseline leg."""
+    import threading
+
+    from dispec_amd.transport.base import KVPayload
+    from dispec_amd.transport.tcp import TcpTransport
+    x = _xfer_setup(torch)
+    tx, rx = TcpTransport(x["a"], "cuda"), TcpTransport(x["b"], "cuda")
+
+    def step():
+        p = KVPayload.export(x["src"], x["src_ids"], x["tokens"], request_id=1)
+        th = threading.Thread(target=tx.send, args=(p,))
+        th.start()
+        got = rx.recv()
+        th.join()
+        got.import_into(x["dst"], x["dst_ids"])
+
+    t = _xfer_time(torch, step)
+    ok = torch.equal(x["dst"].export_contiguous(x["dst_ids"], len(x["tokens"]))[0],
+                     x["src"].export_contiguous(x["src_ids"], len(x["tokens"]))[0])
+    tx.close()
+    rx.close()
+    res = {"xfer_tcp_payload_MB": x["payload_bytes"] / 1e6, "xfer_tcp_ms": t * 1e3,
+           "xfer_tcp_GBps": x["payload_bytes"] / t / 1e9, "xfer_tcp_exact": bool(ok)}
+    del x
+    torch.cuda.empty_cache()
+    return res
+
+
 # ------------------------------------------------------------------------------ config 5
 def bench_c5(torch) -> dict:
     """Gather Qwen3-1.7B paged KV (28 L) of 8 requests x 4096 tokens into contiguous
@@ -707,7 +810,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-aux", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list of c1,c2,c4,c5,skew,ceiling,prefill: run just these auxiliary configs and print "
+                    help="comma list of c1,c2,c4,c5,skew,ceiling,prefill,xfer: run just these auxiliary configs and print "
                          "their numbers (no headline line); 'copy' runs the 1 GiB plain "
                          "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters; "
                          "'graph' times a whole-model decode step, eager against HIP graph")
@@ -724,7 +827,7 @@ def main() -> int:
     torch.cuda.set_device(0)
     configs = (("c1", bench_c1), ("c2", bench_c2), ("c4", bench_c4), ("c5", bench_c5),
                ("skew", bench_skew), ("ceiling", bench_copy_ceiling), ("prefill", bench_prefill),
-               ("copy", bench_copy), ("graph", bench_graph))
+               ("xfer", bench_xfer), ("copy", bench_copy), ("graph", bench_graph))
     if args.only:
         want = set(args.only.split(","))
         aux = {}
@@ -738,7 +841,7 @@ def main() -> int:
     dec = bench_decode(torch, args.steps, args.warmup)
     aux = {}
     if not args.no_aux:
-        for name, fn in configs[:7]:
+        for name, fn in configs[:8]:
             _log(f"config {name}")
             aux.update(fn(torch))
     cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)

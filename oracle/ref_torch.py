@@ -129,3 +129,39 @@ def native_forward(model, token_ids, positions, write_slots, seq_meta, key, valu
         x = x + attn.o_proj(o.reshape(T, H * D))
         x = x + layer.mlp(layer.post_attention_layernorm(x))
     return core.norm(x)
+
+
+# --------------------------------------------- TCP transport (dispec/transport/tcp.py)
+
+
+def tcp_send_pickle(sock, tokens, k, v, meta) -> None:
+    """The reference's TcpTransport.send (tcp.py:61-65, framing :19-21): torch.save of
+    the payload with its tensors moved to the CPU, one `!Q`-framed message."""
+    import io
+    import struct
+    buf = io.BytesIO()
+    torch.save({"tokens": tokens, "k": k.cpu(), "v": v.cpu(), "meta": meta}, buf)
+    data = buf.getvalue()
+    sock.sendall(struct.pack("!Q", len(data)))
+    sock.sendall(data)
+
+
+def tcp_recv_pickle(sock, device):
+    """The reference's TcpTransport.recv (tcp.py:67-70, framing :24-36): read the frame
+    into a bytearray in 1 MiB pieces, torch.load it, move K and V to `device`.  Only ever
+    fed what tcp_send_pickle wrote in the same process (weights_only=True suffices)."""
+    import io
+    import struct
+
+    def recv_n(n):
+        buf = bytearray()
+        while len(buf) < n:
+            chunk = sock.recv(min(n - len(buf), 1 << 20))
+            if not chunk:
+                raise ConnectionError("peer closed during recv")
+            buf.extend(chunk)
+        return bytes(buf)
+
+    (n,) = struct.unpack("!Q", recv_n(8))
+    obj = torch.load(io.BytesIO(recv_n(n)), weights_only=True)
+    return obj["tokens"], obj["k"].to(device), obj["v"].to(device), obj.get("meta", {})
