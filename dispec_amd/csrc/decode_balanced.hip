@@ -4,19 +4,25 @@
 // dispec/engine/triton_attn.py:59-95): one query per sequence, query head h reads KV head
 // h / G (:70), fp32 online softmax (:86-92), output in the cache dtype (:94-95).
 //
-// Work split.  The decode work of one launch is the list of (sequence b, KV head, 16-key
-// unit) triples in sequence-major, then KV-head, then key order; a (sequence, KV head)
-// pair is a "segment".  With C units in all and W workers -- one wave each, at most as
-// many as the GPU holds at once -- worker w takes units [w*C/W, (w+1)*C/W).  Every wave
+// Work split.  The decode work of one launch is the list of (sequence b, group of HG KV
+// heads, 16-key unit) triples in sequence-major, then head-group, then key order; a
+// (sequence, head group) pair is a "segment".  With C units in all and W workers -- one
+// workgroup of HG waves each, at most as many as the GPU holds at once -- worker w takes
+// units [w*C/W, (w+1)*C/W), wave i of it KV head HG*group + i of every unit.  Every wave
 // therefore reads the same number of K/V bytes (to one unit) whatever the spread of context
 // lengths, and all of them finish together: there is no tail of long partitions running on
 // a mostly idle GPU.  C is computed on the device from ctx_lens, so the launch needs no
 // host synchronisation and can be captured in a graph.
 //
 // A worker whose range crosses a segment boundary produces one partial result per piece
-// (row max, row sum, unnormalised accumulator).  Piece (s, w) -- segment s, worker w --
-// is stored at workspace slot s + w: along the unit list the pieces form a staircase in
-// (s, w), so s + w is unique, and the workspace holds B*KVH + W slots.  A segment inside
+// (row max, row sum, unnormalised accumulator) per head.  Piece (s, w) -- segment s,
+// worker w -- is stored at workspace slot s + w (HG heads of G rows each): along the unit
+// list the pieces form a staircase in (s, w), so s + w is unique, and the workspace holds
+// B*KVH/HG + W slots.  Grouping the heads (HG = 4 when KVH allows) makes the waves of a
+// workgroup read the same keys' slot rows side by side: a pure read of config 3's access
+// pattern runs at 6.1 TB/s with all 8 heads of a row read by one workgroup against 5.7
+// TB/s for per-wave slices, and the kernel gains ~3 % (8 heads per workgroup would leave
+// room for only one workgroup per CU at three waves per SIMD: slower).  A segment inside
 // one worker's range is normalised and written to the output by that worker; the combine
 // kernel merges the pieces of every other segment.
 //
@@ -91,8 +97,12 @@ __device__ __forceinline__ int64_t active_workers(int64_t C, int num_workers) {
 // two blocks, whose ids are read as scalars.  kOff32: every element offset into one
 // layer's K or V cache fits in 31 bits, so addresses are a scalar base plus a 32-bit
 // per-lane byte offset.
-template <typename Tag, int D, bool kOff32>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kOcc))) void decode_balanced_kernel(
+// HG: KV heads per workgroup.  The work list is (sequence, group of HG KV heads, unit);
+// a worker is a workgroup of HG waves, wave i taking KV head HG*group + i of every piece,
+// so the waves of a workgroup read the same keys' rows side by side (HG x 256 bytes of
+// each 2 KiB slot row at D 128: the pool's DRAM pages are then read HG slices at a time).
+template <typename Tag, int D, bool kOff32, int HG>
+__global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc))) void decode_balanced_kernel(
     const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
     const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
@@ -106,15 +116,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kOcc))) void
   constexpr int SLAB = 32 * ROWB;   // one 32-key V chunk
   constexpr int VINS = SLAB / 1024; // 1-KiB DMA loads per V chunk
   constexpr int RPI = 1024 / ROWB;  // V rows per DMA load
-  __shared__ __attribute__((aligned(1024))) char slab[SLAB];
+  __shared__ __attribute__((aligned(1024))) char slab[HG][SLAB];
 
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // head within the group
+  const int NG = KVH / HG;                                          // head groups
   const int n = lane & 15;   // packed row = query head kvh*G + n (MFMA N index)
   const int grp = lane >> 4; // lane group: K sub-range of the MFMA operands
   const bool row_ok = n < G;
 
   // ---- this worker's unit range and where it starts
-  const int64_t C = head_units(ctx_lens, B, max_ctx) * KVH;
+  const int64_t C = head_units(ctx_lens, B, max_ctx) * NG;
   const int64_t W = active_workers(C, num_workers);
   const int64_t w = blockIdx.x;
   if (w >= W) return;
@@ -128,25 +140,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kOcc))) void
       const int c = bb < B ? clamp_ctx(ctx_lens[bb], max_ctx) : 0;
       const int v = (c + (1 << kLog2Unit) - 1) >> kLog2Unit;
       const int incl = wave_incl_scan(v);
-      const uint64_t hit = __ballot(int64_t(KVH) * (base + incl) > U);
+      const uint64_t hit = __ballot(int64_t(NG) * (base + incl) > U);
       if (hit) {
         const int f = __builtin_amdgcn_readfirstlane(
             __ffsll(static_cast<unsigned long long>(hit)) - 1);
         b = b0 + f;
         ctx = __builtin_amdgcn_readlane(c, f);
         nb = __builtin_amdgcn_readlane(v, f);
-        U -= int64_t(KVH) * (base + __builtin_amdgcn_readlane(incl, f) - nb);  // inside b
+        U -= int64_t(NG) * (base + __builtin_amdgcn_readlane(incl, f) - nb);  // inside b
         break;
       }
       base += __builtin_amdgcn_readlane(incl, 63);
     }
   }
   if (nb == 0) return;  // unreachable: unit U < C lies in a non-empty sequence
-  int kvh = static_cast<int>(U / nb);
+  int kvg = static_cast<int>(U / nb);
   int u = static_cast<int>(U % nb);
 
   const int bmask = (1 << log2_bs) - 1;
-  char* const slab_l = slab;
+  char* const slab_l = slab[hw];
   auto swz = [](int r, int c) { return c ^ ((2 * ((r >> 2) & 3)) & (CPR - 1)); };
   bool any_bad = false;
 
@@ -156,6 +168,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kOcc))) void
     const int kb = u << kLog2Unit;
     const int ke = min(u1 << kLog2Unit, ctx);
     const bool whole = u == 0 && u1 == nb;
+    const int kvh = kvg * HG + hw;
     const int64_t bt_row = int64_t(b) * bt_stride;
     const int64_t head_off = int64_t(kvh) * kvs_head;
 
@@ -349,7 +362,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kOcc))) void
 #pragma unroll
           for (int j = 0; j < 4; ++j) o[16 * nt + j] = narrow<Tag>(acc[nt][j] * inv);
       } else {
-        const int64_t row = (int64_t(b) * KVH + kvh + w) * G + n;  // slot s + w, row n
+        // piece (segment s = b*NG + kvg, worker w) is slot s + w; its head hw, row n
+        const int64_t row = ((int64_t(b) * NG + kvg + w) * HG + hw) * G + n;
         float* a = ws_acc + row * D + 4 * grp;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<f32x4*>(a + 16 * nt) = acc[nt];
@@ -362,11 +376,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(kOcc))) void
 
     left -= u1 - u;
     if (left <= 0) break;
-    // next segment: the next KV head of b, or the first KV head of the next non-empty
-    // sequence (one exists: units remain)
+    // next segment: the next head group of b, or the first of the next non-empty sequence
+    // (one exists: units remain)
     u = 0;
-    if (++kvh == KVH) {
-      kvh = 0;
+    if (++kvg == NG) {
+      kvg = 0;
       do {
         if (++b >= B) break;
         ctx = clamp_ctx(ctx_lens[b], max_ctx);
@@ -385,7 +399,7 @@ template <typename Tag, int D>
 __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t max_ctx,
-    int32_t num_workers, uint16_t* __restrict__ out, int64_t osb, int64_t osh,
+    int32_t num_workers, int32_t HG, uint16_t* __restrict__ out, int64_t osb, int64_t osh,
     int32_t* __restrict__ err_count) {
   constexpr int NV = D > 64 ? 2 : 1;  // dims per lane: lane, lane + 64
   __shared__ float s_w[4][64];
@@ -411,16 +425,17 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
     }
     return;
   }
-  const int64_t C = total * KVH;
+  const int NG = KVH / HG;
+  const int64_t C = total * NG;
   const int64_t W = active_workers(C, num_workers);
-  const int kvh = h / G, g = h % G;
-  const int64_t cs = int64_t(KVH) * pre + int64_t(kvh) * nb, ce = cs + nb;
+  const int kvh = h / G, g = h % G, kvg = kvh / HG, hw = kvh % HG;
+  const int64_t cs = int64_t(NG) * pre + int64_t(kvg) * nb, ce = cs + nb;
   const int64_t w0 = ((cs + 1) * W - 1) / C, w1 = (ce * W - 1) / C;
   if (w0 == w1) return;  // one worker covered the segment and wrote the output
   const int np = static_cast<int>(w1 - w0 + 1);
-  // piece p is slot (b*KVH + kvh) + w0 + p; its row g
-  const int64_t row0 = (int64_t(b) * KVH + kvh + w0) * G + g;
-  const int64_t pstride = G;  // rows between consecutive slots
+  // piece p is slot (b*NG + kvg) + w0 + p; its head hw, row g
+  const int64_t row0 = ((int64_t(b) * NG + kvg + w0) * HG + hw) * G + g;
+  const int64_t pstride = int64_t(HG) * G;  // rows between consecutive slots
   float M = -INFINITY;
   for (int p = lane; p < np; p += 64) M = fmaxf(M, ws_ml[2 * (row0 + p * pstride)]);
 #pragma unroll
@@ -476,6 +491,33 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
   }
 }
 
+template <typename Tag, int D, int HG>
+int launch_balanced_hg(int W, const uint16_t* q, int64_t qsb, int64_t qsh, const uint16_t* kc,
+                       const uint16_t* vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
+                       const int32_t* bt, int64_t bt_stride, int32_t log2_bs,
+                       const int32_t* ctx_lens, int32_t B, int32_t KVH, int32_t G,
+                       int32_t max_ctx, float scale_log2, float* ws_acc, float* ws_ml,
+                       uint16_t* out, int64_t osb, int64_t osh, int32_t* err_count,
+                       hipStream_t s) {
+  const int Wg = W / HG > 0 ? W / HG : 1;  // workgroups of HG waves
+  // largest element offset: last slot's last head's row end
+  const bool off32 = num_slots * kvs_slot + KVH * kvs_head + D < (int64_t(1) << 31);
+  if (off32)
+    decode_balanced_kernel<Tag, D, true, HG><<<dim3(static_cast<unsigned>(Wg)), 64 * HG, 0, s>>>(
+        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens, B,
+        KVH, G, max_ctx, scale_log2, Wg, ws_acc, ws_ml, out, osb, osh, err_count);
+  else
+    decode_balanced_kernel<Tag, D, false, HG><<<dim3(static_cast<unsigned>(Wg)), 64 * HG, 0, s>>>(
+        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens, B,
+        KVH, G, max_ctx, scale_log2, Wg, ws_acc, ws_ml, out, osb, osh, err_count);
+  const int st = dsp_launch_status();
+  if (st != DSP_OK) return st;
+  const int Hq = KVH * G;
+  decode_balanced_combine_kernel<Tag, D><<<dim3((Hq + 3) / 4, B), 256, 0, s>>>(
+      ws_acc, ws_ml, ctx_lens, B, KVH, G, max_ctx, Wg, HG, out, osb, osh, err_count);
+  return dsp_launch_status();
+}
+
 template <typename Tag, int D>
 int launch_balanced_d(int W, const uint16_t* q, int64_t qsb, int64_t qsh, const uint16_t* kc,
                       const uint16_t* vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
@@ -483,22 +525,24 @@ int launch_balanced_d(int W, const uint16_t* q, int64_t qsb, int64_t qsh, const 
                       const int32_t* ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t max_ctx,
                       float scale_log2, float* ws_acc, float* ws_ml, uint16_t* out, int64_t osb,
                       int64_t osh, int32_t* err_count, hipStream_t s) {
-  // largest element offset: last slot's last head's row end
-  const bool off32 = num_slots * kvs_slot + KVH * kvs_head + D < (int64_t(1) << 31);
-  if (off32)
-    decode_balanced_kernel<Tag, D, true><<<dim3(static_cast<unsigned>(W)), 64, 0, s>>>(
-        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens, B,
-        KVH, G, max_ctx, scale_log2, W, ws_acc, ws_ml, out, osb, osh, err_count);
-  else
-    decode_balanced_kernel<Tag, D, false><<<dim3(static_cast<unsigned>(W)), 64, 0, s>>>(
-        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens, B,
-        KVH, G, max_ctx, scale_log2, W, ws_acc, ws_ml, out, osb, osh, err_count);
-  const int st = dsp_launch_status();
-  if (st != DSP_OK) return st;
-  const int Hq = KVH * G;
-  decode_balanced_combine_kernel<Tag, D><<<dim3((Hq + 3) / 4, B), 256, 0, s>>>(
-      ws_acc, ws_ml, ctx_lens, B, KVH, G, max_ctx, W, out, osb, osh, err_count);
-  return dsp_launch_status();
+  switch (dsp_detail::balanced_head_group(KVH)) {
+    case 8:
+      return launch_balanced_hg<Tag, D, 8>(W, q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head,
+                                           bt, bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx,
+                                           scale_log2, ws_acc, ws_ml, out, osb, osh, err_count, s);
+    case 4:
+      return launch_balanced_hg<Tag, D, 4>(W, q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head,
+                                           bt, bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx,
+                                           scale_log2, ws_acc, ws_ml, out, osb, osh, err_count, s);
+    case 2:
+      return launch_balanced_hg<Tag, D, 2>(W, q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head,
+                                           bt, bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx,
+                                           scale_log2, ws_acc, ws_ml, out, osb, osh, err_count, s);
+    default:
+      return launch_balanced_hg<Tag, D, 1>(W, q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head,
+                                           bt, bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx,
+                                           scale_log2, ws_acc, ws_ml, out, osb, osh, err_count, s);
+  }
 }
 
 template <typename Tag, typename... A>
@@ -524,6 +568,11 @@ int device_cus() {
   return cus;
 }
 
+
+// KV heads per workgroup of the balanced kernel: the largest of 4, 2, 1 dividing KVH.
+int balanced_head_group(int32_t KVH) {
+  return KVH % 4 == 0 ? 4 : (KVH % 2 == 0 ? 2 : 1);
+}
 
 bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
                              int32_t block_size) {

@@ -26,6 +26,7 @@ int mq_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const u
 bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
                              int32_t block_size);
 int32_t balanced_workers(int32_t B, int32_t KVH, int32_t max_ctx);
+int balanced_head_group(int32_t KVH);
 size_t balanced_workspace_bytes(int32_t B, int32_t KVH, int32_t G, int32_t D, int32_t max_ctx);
 int balanced_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
                     const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,
