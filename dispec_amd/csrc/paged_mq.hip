@@ -46,9 +46,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
     int32_t G, float scale_log2, int32_t P, int32_t num_parts, int32_t tiles_max,
-    int32_t first_part, int32_t prefix_tokens, float* __restrict__ ws_acc,
-    float* __restrict__ ws_ml, uint16_t* __restrict__ out, int64_t ost, int64_t osh,
-    int32_t* __restrict__ err_count) {
+    float* __restrict__ ws_acc, float* __restrict__ ws_ml, uint16_t* __restrict__ out,
+    int64_t ost, int64_t osh, int32_t* __restrict__ err_count) {
   constexpr int NKK = D / 32;        // 32-dim K steps of the score MFMA
   constexpr int NT = D / 16;         // 16-dim output tiles
   constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
@@ -66,12 +65,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   auto s_acc = reinterpret_cast<float (*)[16][D + 1]>(s_raw);
   char* const slab_base = s_raw;
 
-  // Partitions below first_part (a shared prefix, computed by the prefix pass of
-  // dsp_paged_mq_attention_shared_prefix) are not launched.
-  const int nsplit = num_parts - first_part;
+  const int part = blockIdx.x % num_parts, tile = blockIdx.x / num_parts;
+  const int kvh = blockIdx.y, b = blockIdx.z;
   const int KVH = gridDim.y;
-  int xw = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int part = first_part + xw % nsplit, tile = xw / nsplit;
   const int q0 = kDecode ? b : cu_q[b];
   const int qlen = kDecode ? 1 : cu_q[b + 1] - q0;
   int ctx = ctx_lens[b];
@@ -84,10 +80,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
       if (threadIdx.x == 0 && part == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
       ctx = ctx < 0 ? 0 : max_ctx;
     }
-  } else if (ctx > max_ctx || ctx < qlen || ctx - qlen < prefix_tokens) {
+  } else if (ctx > max_ctx || ctx < qlen) {
     bad = true;
-    if (threadIdx.x == 0 && tile == 0 && part == first_part && kvh == 0 && err_count)
-      atomicAdd(err_count, 1);
+    if (threadIdx.x == 0 && tile == 0 && part == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
     ctx = 0;  // no keys: rows are written as zeros
   }
 
@@ -103,7 +98,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   const int kend = bad ? 0 : ctx - qlen + r_last / G + 1;  // keys any row of the tile sees
   // Split-K: this workgroup covers keys [kbeg, kfin) of the tile's causal range.
   const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
-  if (bad ? part != first_part : part >= nparts) return;  // a bad tile: one writer of zeros
+  if (part >= nparts) return;
   const int kbeg = part * P;
   const int kfin = min(kbeg + P, kend);
   const int64_t bt_row = int64_t(b) * bt_stride;
@@ -319,7 +314,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
     int32_t G, int32_t P, int32_t num_parts, int32_t tiles_max, int32_t prefix_tokens,
-    uint16_t* __restrict__ out, int64_t ost, int64_t osh) {
+    int32_t fixed_parts, uint16_t* __restrict__ out, int64_t ost, int64_t osh) {
   constexpr int R = 256 / D;            // rows per workgroup
   constexpr int W = D < 64 ? D : 64;    // lanes that reduce one row's partition weights
   __shared__ float s_w[R][kMaxParts];
@@ -335,7 +330,8 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
     return;
   const int r_last = min(r0 + 15, rows - 1);
   const int kend = ctx - qlen + r_last / G + 1;
-  const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
+  // a shared-prefix launch writes fixed_parts partitions for every row
+  const int nparts = fixed_parts > 0 ? fixed_parts : (kend > 0 ? (kend + P - 1) / P : 1);
   if (nparts <= 1) return;  // written directly by the attention kernel
   const int64_t slot0 = ((int64_t(b) * KVH + kvh) * tiles_max + tile) * num_parts;
   const int rl = threadIdx.x / D, d = threadIdx.x % D;
@@ -418,13 +414,13 @@ int mq_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const u
     return launch_mq<Bf16Tag, true>(D, grid, s, q, q_stride_b, q_stride_h, k_cache, v_cache,
                                     num_slots, kv_stride_slot, kv_stride_head, block_table,
                                     bt_stride, log2_bs, no_cu, ctx_lens, max_ctx, G, scale_log2, P,
-                                    num_parts, int32_t(1), int32_t(0), int32_t(0), ws_acc, ws_ml,
-                                    out, o_stride_b, o_stride_h, err_count);
+                                    num_parts, int32_t(1), ws_acc, ws_ml, out, o_stride_b,
+                                    o_stride_h, err_count);
   return launch_mq<F16Tag, true>(D, grid, s, q, q_stride_b, q_stride_h, k_cache, v_cache,
                                  num_slots, kv_stride_slot, kv_stride_head, block_table, bt_stride,
                                  log2_bs, no_cu, ctx_lens, max_ctx, G, scale_log2, P, num_parts,
-                                 int32_t(1), int32_t(0), int32_t(0), ws_acc, ws_ml, out,
-                                 o_stride_b, o_stride_h, err_count);
+                                 int32_t(1), ws_acc, ws_ml, out, o_stride_b, o_stride_h,
+                                 err_count);
 }
 
 }  // namespace dsp_detail
@@ -538,41 +534,49 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
   const int32_t tm = static_cast<int32_t>(tiles);
   const bool f16 = dtype == DSP_F16;
   int st = DSP_OK;
-  if (prefix_tokens > 0)
+  int ws_parts = num_parts, fixed_parts = 0;
+  if (prefix_tokens > 0) {
+    // prefix and suffix tiles in one launch, then a merge of first_part + 1 partitions
+    ws_parts = fixed_parts = first_part + 1;
+    DSP_HOST_CHECK(dsp_detail::shared_prefix_grid(B, G, max_q_len, P, prefix_tokens) <
+                       (int64_t(1) << 31),
+                   DSP_EINVAL);
     st = dsp_detail::prefill_shared_prefix(qh, q_stride_t, q_stride_h, kh, vh, num_slots,
-                                           kv_stride_slot, kv_stride_head, block_table, lbs, cu_q,
-                                           B, KVH, G, D, scale_log2, max_q_len, max_ctx, P,
-                                           num_parts, tm, prefix_tokens, ws_acc, ws_ml, f16, s);
-  if (st != DSP_OK) return st;
-  if (prefix_tokens == 0 && dsp_detail::prefill_applies(D, block_size, int64_t(max_q_len) * G,
-                                                         num_slots, kv_stride_slot)) {
+                                           kv_stride_slot, kv_stride_head, block_table, bt_stride,
+                                           lbs, cu_q, ctx_lens, B, KVH, G, D, scale_log2,
+                                           max_q_len, max_ctx, P, tm, prefix_tokens, ws_acc,
+                                           ws_ml, oh, o_stride_t, o_stride_h, f16, err_count, s);
+  } else if (dsp_detail::prefill_applies(D, block_size, int64_t(max_q_len) * G, num_slots,
+                                         kv_stride_slot)) {
     st = dsp_detail::prefill_attention(qh, q_stride_t, q_stride_h, kh, vh, num_slots,
                                        kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs,
                                        cu_q, ctx_lens, B, KVH, G, D, scale_log2, max_q_len, max_ctx,
                                        P, num_parts, tm, ws_acc, ws_ml, oh, o_stride_t, o_stride_h,
                                        f16, err_count, s);
   } else {
-    dim3 grid(static_cast<unsigned>(tiles * (num_parts - first_part)), static_cast<unsigned>(KVH),
+    dim3 grid(static_cast<unsigned>(tiles * num_parts), static_cast<unsigned>(KVH),
               static_cast<unsigned>(B));
     if (!f16)
       st = launch_mq<Bf16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
                               kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
-                              ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, first_part,
-                              prefix_tokens, ws_acc, ws_ml, oh, o_stride_t, o_stride_h, err_count);
+                              ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, ws_acc, ws_ml,
+                              oh, o_stride_t, o_stride_h, err_count);
     else
       st = launch_mq<F16Tag>(D, grid, s, qh, q_stride_t, q_stride_h, kh, vh, num_slots,
                              kv_stride_slot, kv_stride_head, block_table, bt_stride, lbs, cu_q,
-                             ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, first_part,
-                             prefix_tokens, ws_acc, ws_ml, oh, o_stride_t, o_stride_h, err_count);
+                             ctx_lens, max_ctx, G, scale_log2, P, num_parts, tm, ws_acc, ws_ml,
+                             oh, o_stride_t, o_stride_h, err_count);
   }
-  if (st != DSP_OK || num_parts <= 1) return st;
+  if (st != DSP_OK || ws_parts <= 1) return st;
   dim3 cgrid(static_cast<unsigned>(tiles * 16 / (256 / D)), static_cast<unsigned>(KVH),
              static_cast<unsigned>(B));
   if (!f16)
     return launch_mq_combine<Bf16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
-                                      num_parts, tm, prefix_tokens, oh, o_stride_t, o_stride_h);
+                                      ws_parts, tm, prefix_tokens, fixed_parts, oh, o_stride_t,
+                                      o_stride_h);
   return launch_mq_combine<F16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
-                                   num_parts, tm, prefix_tokens, oh, o_stride_t, o_stride_h);
+                                   ws_parts, tm, prefix_tokens, fixed_parts, oh, o_stride_t,
+                                   o_stride_h);
 }
 
 }  // namespace

@@ -70,12 +70,15 @@ __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 
-// kShared: the prefix pass of a shared-prefix (cascade) launch.  Packed row r is token
-// r / G of the whole batch (every sequence's queries), query head kvh*G + r % G; the keys
-// are the first prefix_tokens of block-table row 0, which every sequence shares and every
-// query sees whole (no mask).  Partition `part` covers keys [part*P, part*P + P) and is
-// written, for every row, to that row's own (sequence, 16-row tile) slot of the merge
-// layout; the sequences' suffix partitions follow it.
+// kShared: a shared-prefix (cascade) launch, two kinds of workgroup in one grid.  For
+// x < prefix_x (per KV head) a workgroup is a prefix tile: packed row r is token r / G of
+// the whole batch (every sequence's queries), query head kvh*G + r % G; the keys are the
+// first prefix_tokens of block-table row 0, which every sequence shares and every query
+// sees whole (no mask); partition `part` covers keys [part*P, part*P + P) and is written,
+// for every row, to that row's own (sequence, 16-row tile) slot of the merge layout.  The
+// other workgroups are suffix tiles: one sequence's rows over its keys from prefix_tokens
+// on (causal), written as partition prefix_tokens / P.  Both kinds run side by side; the
+// merge then folds prefix_tokens / P + 1 partitions per row.
 template <typename Tag, int D, bool kShared>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t qst, int64_t qsh, const uint16_t* __restrict__ kc,
@@ -85,7 +88,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     int32_t G, float scale_log2, int32_t P, int32_t num_parts, int32_t tiles16_max,
     float* __restrict__ ws_acc, float* __restrict__ ws_ml, uint16_t* __restrict__ out,
     int64_t ost, int64_t osh, int32_t* __restrict__ err_count, int32_t nseq,
-    int32_t prefix_tokens, int32_t ws_parts) {
+    int32_t prefix_tokens, int32_t ws_parts, int32_t prefix_x) {
   constexpr int NKS = D / 16;        // 16-dim steps of the score MFMA
   constexpr int NDT = D / 32;        // 32-dim output tiles
   constexpr int CPR = D / 8;         // 16-byte chunks per K/V row
@@ -107,11 +110,27 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int64_t q8 = nwg / 8, r8 = nwg % 8, xcd = lin % 8, pos = lin / 8;
   const int64_t lg = xcd < r8 ? xcd * (q8 + 1) + pos : r8 * (q8 + 1) + (xcd - r8) * q8 + pos;
   const int xl = int(lg % X);
-  const int kvh = int((lg / X) % KVH), b = int(lg / X / KVH);
-  const int ntiles = X / num_parts;
-  const int part = xl % num_parts, tile = ntiles - 1 - xl / num_parts;
-  int q0, qlen, ctx, kend;
+  const int kvh = int((lg / X) % KVH);
+  int b = int(lg / X / KVH), part, tile;
+  bool pre = false;  // a prefix tile of a shared-prefix launch
   if constexpr (kShared) {
+    pre = xl < prefix_x;
+    if (pre) {
+      part = xl % num_parts;
+      tile = prefix_x / num_parts - 1 - xl / num_parts;
+    } else {
+      const int tiles_s = (X - prefix_x) / nseq, idx = xl - prefix_x;
+      b = idx / tiles_s;
+      tile = tiles_s - 1 - idx % tiles_s;
+      part = prefix_tokens / P;
+    }
+  } else {
+    const int ntiles = X / num_parts;
+    part = xl % num_parts;
+    tile = ntiles - 1 - xl / num_parts;
+  }
+  int q0, qlen, ctx, kend = 0;
+  if (pre) {
     // all tokens of the batch; the causal limit never binds (ctx - qlen + qi >= max_ctx)
     q0 = 0;
     qlen = cu_q[nseq];
@@ -128,9 +147,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int rows = qlen * G;
   const int r0 = tile * kRows;
   if (qlen <= 0 || r0 >= rows) return;
-  if constexpr (!kShared) {
-    if (ctx > max_ctx || ctx < qlen) {  // bad lengths: counted once, the rows are zeros
-      if (part != 0) return;
+  if (!pre) {
+    // bad lengths (and, in a shared-prefix launch, queries that start inside the prefix):
+    // counted once, the rows are zeros
+    if (ctx > max_ctx || ctx < qlen || (kShared && ctx - qlen < prefix_tokens)) {
+      if (!kShared && part != 0) return;
       if (threadIdx.x == 0 && tile == 0 && kvh == 0 && err_count) atomicAdd(err_count, 1);
       for (int i = threadIdx.x; i < kRows * D; i += kThreads) {
         const int rr = r0 + i / D;
@@ -142,9 +163,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const int r_last = min(r0 + kRows - 1, rows - 1);
     kend = ctx - qlen + r_last / G + 1;  // keys any row of the tile sees
   }
-  const int kbeg = part * P;
+  // a suffix tile covers everything past the prefix in one partition
+  const bool suffix = kShared && !pre;
+  const int kbeg = suffix ? prefix_tokens : part * P;
   if (kbeg >= kend) return;
-  const int kfin = min(kbeg + P, kend);
+  const int kfin = suffix ? kend : min(kbeg + P, kend);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -327,7 +350,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   lpart += dsp_shfl_xor(lpart, 32);
   if (!row_ok) return;
   int sb = b, lr = r;  // the row's sequence and its packed row there
-  if constexpr (kShared) {
+  if (pre) {
     int lo = 0, hi = nseq - 1;  // last sequence whose first token is <= qi
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -410,27 +433,36 @@ int prefill_attention(const uint16_t* q, int64_t q_stride_t, int64_t q_stride_h,
                                num_slots, kv_stride_slot, kv_stride_head, block_table, bt_stride,
                                log2_bs, cu_q, ctx_lens, max_ctx, G, scale_log2, P, num_parts,
                                tiles16_max, ws_acc, ws_ml, out, o_stride_t, o_stride_h,
-                               err_count, B, int32_t(0), num_parts);
+                               err_count, B, int32_t(0), num_parts, int32_t(0));
 }
 
 int prefill_shared_prefix(const uint16_t* q, int64_t q_stride_t, int64_t q_stride_h,
                           const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,
                           int64_t kv_stride_slot, int64_t kv_stride_head,
-                          const int32_t* block_table, int32_t log2_bs, const int32_t* cu_q,
-                          int32_t B, int32_t KVH, int32_t G, int32_t D, float scale_log2,
-                          int32_t max_q_len, int32_t max_ctx, int32_t P, int32_t num_parts,
-                          int32_t tiles16_max, int32_t prefix_tokens, float* ws_acc,
-                          float* ws_ml, bool f16, hipStream_t s) {
-  const int64_t tiles = (int64_t(B) * max_q_len * G + kRows - 1) / kRows;
+                          const int32_t* block_table, int64_t bt_stride, int32_t log2_bs,
+                          const int32_t* cu_q, const int32_t* ctx_lens, int32_t B, int32_t KVH,
+                          int32_t G, int32_t D, float scale_log2, int32_t max_q_len,
+                          int32_t max_ctx, int32_t P, int32_t tiles16_max,
+                          int32_t prefix_tokens, float* ws_acc, float* ws_ml, uint16_t* out,
+                          int64_t o_stride_t, int64_t o_stride_h, bool f16, int32_t* err_count,
+                          hipStream_t s) {
   const int32_t prefix_parts = prefix_tokens / P;
-  dim3 grid(static_cast<unsigned>(tiles * prefix_parts), static_cast<unsigned>(KVH), 1u);
-  int32_t* no_err = nullptr;
-  uint16_t* no_out = nullptr;
+  const int64_t tiles_p = (int64_t(B) * max_q_len * G + kRows - 1) / kRows;
+  const int64_t prefix_x = tiles_p * prefix_parts;
+  const int64_t suffix_x = int64_t(B) * prefill_tiles(max_q_len, G);
+  dim3 grid(static_cast<unsigned>(prefix_x + suffix_x), static_cast<unsigned>(KVH), 1u);
   return launch_prefill<true>(D, f16, grid, s, q, q_stride_t, q_stride_h, k_cache, v_cache,
-                              num_slots, kv_stride_slot, kv_stride_head, block_table, int64_t(0),
-                              log2_bs, cu_q, cu_q, max_ctx, G, scale_log2, P, prefix_parts,
-                              tiles16_max, ws_acc, ws_ml, no_out, int64_t(0), int64_t(0), no_err,
-                              B, prefix_tokens, num_parts);
+                              num_slots, kv_stride_slot, kv_stride_head, block_table, bt_stride,
+                              log2_bs, cu_q, ctx_lens, max_ctx, G, scale_log2, P, prefix_parts,
+                              tiles16_max, ws_acc, ws_ml, out, o_stride_t, o_stride_h, err_count,
+                              B, prefix_tokens, prefix_parts + 1,
+                              static_cast<int32_t>(prefix_x));
+}
+
+int64_t shared_prefix_grid(int32_t B, int32_t G, int32_t max_q_len, int32_t P,
+                           int32_t prefix_tokens) {
+  const int64_t tiles_p = (int64_t(B) * max_q_len * G + kRows - 1) / kRows;
+  return tiles_p * (prefix_tokens / P) + int64_t(B) * prefill_tiles(max_q_len, G);
 }
 
 bool shared_prefix_applies(int32_t D, int32_t block_size, int32_t B, int64_t num_slots,
