@@ -789,9 +789,9 @@ def bench_copy_ceiling(torch) -> dict:
 
 
 def _traffic_per_launch():
-    """HBM bytes per decode launch (FETCH_SIZE + WRITE_SIZE of paged_decode_kernel and
-    decode_combine_kernel, each scaled by the copy calibration), as measured by the
-    rocprofv3 passes recorded in profiles/decode_c3_traffic.md; None if absent."""
+    """HBM bytes per decode launch (FETCH_SIZE + WRITE_SIZE of the balanced decode kernel
+    and its combine, each scaled by the copy calibration), as measured by the rocprofv3
+    passes recorded in profiles/decode_c3_traffic.md; None if absent."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         "decode_c3_traffic.md")
     if not os.path.exists(path):
