@@ -430,36 +430,28 @@ extern "C" int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH,
   if (B <= 0 || KVH <= 0 || Hq % KVH != 0 || max_q_len <= 0 || max_ctx <= 0) return 128;
   const int G = Hq / KVH;
   const int64_t whole = (int64_t(max_ctx) + 127) / 128 * 128;
-  if (int64_t(max_q_len) * G >= 128) {
-    // Long query blocks run on the 128-row prefill tile, two resident per CU at D 128 and
-    // four at D 64 (LDS and registers).  Pick the
-    // partition count n that minimises (rounds of resident tiles) x (keys per tile + a
-    // fixed cost) + the merge's cost per partition, in units of keys: a split pays only
-    // when it fills a round of the machine that would otherwise idle.
-    const int64_t base = int64_t(B) * KVH * dsp_detail::prefill_tiles(max_q_len, G);
-    const int64_t slots = (D <= 64 ? 4 : 2) * int64_t(dsp_detail::device_cus());
-    if (base >= slots) return static_cast<int32_t>(whole);
-    int64_t best_p = whole, best_cost = INT64_MAX;
-    for (int n = 1; n <= kMaxParts; ++n) {
-      const int64_t p = ((max_ctx + n - 1) / n + 127) / 128 * 128;
-      const int64_t parts = (max_ctx + p - 1) / p;
-      if (parts != n) continue;  // the same partition as a smaller n
-      const int64_t rounds = (base * parts + slots - 1) / slots;
-      const int64_t cost = rounds * (p + 256) + (parts > 1 ? 192 + 48 * parts : 0);
-      if (cost < best_cost) best_cost = cost, best_p = p;
-    }
-    return static_cast<int32_t>(best_p);
+  // Pick the partition count n that minimises (rounds of resident workgroups) x (keys per
+  // workgroup + a fixed cost) + the merge's cost per partition, in units of keys: a split
+  // pays only when it fills a round of the machine that would otherwise idle.  Long query
+  // blocks run on the 128-row prefill tile, two resident per CU at D 128 and four at D 64
+  // (LDS and registers); short ones (verify) on 16-row tiles, three per CU.  (Verify, 32
+  // sequences of ~2.3k tokens, Qwen3 heads: 62-65 us with 3 partitions, 68-71 with 7;
+  // 64 sequences of 300-700 tokens: 29 us unsplit, 37-42 with 2-3 partitions.)
+  const bool long_q = int64_t(max_q_len) * G >= 128;
+  const int64_t base = int64_t(B) * KVH *
+                       (long_q ? dsp_detail::prefill_tiles(max_q_len, G) : mq_tiles(max_q_len, G));
+  const int64_t slots = (long_q ? (D <= 64 ? 4 : 2) : 3) * int64_t(dsp_detail::device_cus());
+  if (base >= slots) return static_cast<int32_t>(whole);
+  int64_t best_p = whole, best_cost = INT64_MAX;
+  for (int n = 1; n <= kMaxParts; ++n) {
+    const int64_t p = ((max_ctx + n - 1) / n + 127) / 128 * 128;
+    const int64_t parts = (max_ctx + p - 1) / p;
+    if (parts != n) continue;  // the same partition as a smaller n
+    const int64_t rounds = (base * parts + slots - 1) / slots;
+    const int64_t cost = rounds * (p + 256) + (parts > 1 ? 192 + 48 * parts : 0);
+    if (cost < best_cost) best_cost = cost, best_p = p;
   }
-  // Short ones run on 16-row tiles: aim at ~2048 workgroups, partitions of at least 128
-  // keys (one step of every wave).
-  const int64_t base = int64_t(B) * KVH * mq_tiles(max_q_len, G);
-  if (base >= 1024) return static_cast<int32_t>(whole);
-  int64_t want = (2048 + base - 1) / base;
-  if (want > kMaxParts) want = kMaxParts;
-  int64_t P = (max_ctx + want - 1) / want;
-  P = (P + 127) / 128 * 128;
-  if (P < 128) P = 128;
-  return static_cast<int32_t>(P < whole ? P : whole);
+  return static_cast<int32_t>(best_p);
 }
 
 extern "C" size_t dsp_paged_mq_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,

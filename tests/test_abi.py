@@ -86,8 +86,12 @@ def test_partition_and_workspace_sizing(lib):
     assert lib.dsp_paged_mq_partition_tokens(2, 12, 2, 128, 512, 8192) == 1664
     assert lib.dsp_paged_mq_partition_tokens(4, 32, 8, 128, 512, 4096) == 4096  # 512 tiles
     assert lib.dsp_paged_mq_partition_tokens(2, 16, 4, 64, 1024, 4096) == 1024  # 4 per CU
-    # short ones (verify) on 16-row tiles: ~2048 workgroups, partitions >= 128 keys
-    assert lib.dsp_paged_mq_partition_tokens(8, 16, 8, 128, 5, 2560) == 128
+    # short ones (verify) on 16-row tiles, three resident per CU: 256 tiles of ~2.6k keys
+    # fill one round in 3 partitions; 512 tiles of 704 keys stay whole (a split would need
+    # a second round and the merge)
+    assert lib.dsp_paged_mq_partition_tokens(32, 16, 8, 128, 5, 2688) == 896
+    assert lib.dsp_paged_mq_partition_tokens(64, 16, 8, 128, 5, 704) == 768
+    assert lib.dsp_paged_mq_partition_tokens(8, 16, 8, 128, 5, 2560) == 384
     assert lib.dsp_paged_decode_workspace_bytes(16, 32, 8, 128, 32768, 512) == 16 * 32 * 64 * 130 * 4
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, 512) == 0   # one partition
     # automatic split: room for the balanced split (B*KVH + waves slots of G rows) and for
