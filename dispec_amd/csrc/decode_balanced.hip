@@ -392,9 +392,13 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
   if (err_count && __ballot(any_bad) && lane == 0) atomicAdd(err_count, 1);
 }
 
-// One wave per (sequence b, query head h).  Merges the pieces of segment (b, h / G) when
-// more than one worker covered it, writes zeros for an empty context, and counts a
-// context length outside [0, max_ctx] once per sequence.
+// One workgroup (4 waves) per (sequence b, query head h).  Merges the pieces of segment
+// (b, h / G) when more than one worker covered it, writes zeros for an empty context, and
+// counts a context length outside [0, max_ctx] once per sequence.  A long context among
+// short ones spans hundreds of workers, so the pieces are split over the 4 waves, each
+// lane keeping 16 piece rows in flight; the waves' sums meet in LDS.
+constexpr int kCombineMaxPieces = 4 * kOcc * 1024;  // workers of a launch: <= 4 x kOcc x CUs
+
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
@@ -402,10 +406,12 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
     int32_t num_workers, int32_t HG, uint16_t* __restrict__ out, int64_t osb, int64_t osh,
     int32_t* __restrict__ err_count) {
   constexpr int NV = D > 64 ? 2 : 1;  // dims per lane: lane, lane + 64
-  __shared__ float s_w[4][64];
+  constexpr int kInFlight = 16;       // piece rows loaded per lane before their FMAs
+  __shared__ float s_w[kCombineMaxPieces];
+  __shared__ float s_acc[4][NV * 64];
+  __shared__ float s_red[4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int h = blockIdx.x * 4 + wave, b = blockIdx.y;
-  if (h >= KVH * G) return;
+  const int h = blockIdx.x, b = blockIdx.y;
   int64_t total = 0, pre = 0;
   for (int b0 = 0; b0 < B; b0 += 64) {
     const int bb = b0 + lane;
@@ -414,15 +420,12 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
     pre += wave_sum(bb < b ? v : 0);
   }
   const int raw = ctx_lens[b];
-  if (h == 0 && lane == 0 && err_count && (raw < 0 || raw > max_ctx)) atomicAdd(err_count, 1);
+  if (h == 0 && threadIdx.x == 0 && err_count && (raw < 0 || raw > max_ctx))
+    atomicAdd(err_count, 1);
   const int nb = units_of(raw, max_ctx);
   uint16_t* o = out + int64_t(b) * osb + int64_t(h) * osh;
-  const bool act = lane < D;
   if (nb == 0) {
-    if (act) {
-#pragma unroll
-      for (int j = 0; j < NV; ++j) o[lane + 64 * j] = 0;
-    }
+    if (threadIdx.x < D) o[threadIdx.x] = 0;
     return;
   }
   const int NG = KVH / HG;
@@ -436,58 +439,61 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
   // piece p is slot (b*NG + kvg) + w0 + p; its head hw, row g
   const int64_t row0 = ((int64_t(b) * NG + kvg + w0) * HG + hw) * G + g;
   const int64_t pstride = int64_t(HG) * G;  // rows between consecutive slots
+
+  // row max over the pieces, then their weights 2^(m_p - M) and the weighted row sum
   float M = -INFINITY;
-  for (int p = lane; p < np; p += 64) M = fmaxf(M, ws_ml[2 * (row0 + p * pstride)]);
+  for (int p = threadIdx.x; p < np; p += 256) M = fmaxf(M, ws_ml[2 * (row0 + p * pstride)]);
 #pragma unroll
   for (int mask = 1; mask < 64; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
+  if (lane == 0) s_red[wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f, A[NV];
-#pragma unroll
-  for (int j = 0; j < NV; ++j) A[j] = 0.f;
-  for (int p0 = 0; p0 < np; p0 += 64) {
-    const int p = p0 + lane;
-    float wgt = 0.f;
-    if (p < np) {
-      const int64_t r = row0 + p * pstride;
-      wgt = dsp_exp2(ws_ml[2 * r] - Mu);
-      L = fmaf(ws_ml[2 * r + 1], wgt, L);
-    }
-    s_w[wave][lane] = wgt;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int cnt = min(64, np - p0);
-    const float* src = ws_acc + (row0 + int64_t(p0) * pstride) * D + (act ? lane : 0);
-    const int64_t step = pstride * D;
-    int k = 0;
-    for (; k + 8 <= cnt; k += 8) {
-      float v[8][NV];
-#pragma unroll
-      for (int uu = 0; uu < 8; ++uu)
-#pragma unroll
-        for (int j = 0; j < NV; ++j) v[uu][j] = src[int64_t(k + uu) * step + 64 * j];
-#pragma unroll
-      for (int uu = 0; uu < 8; ++uu) {
-        const float wk = s_w[wave][k + uu];
-#pragma unroll
-        for (int j = 0; j < NV; ++j) A[j] = fmaf(v[uu][j], wk, A[j]);
-      }
-    }
-    for (; k < cnt; ++k) {
-      const float wk = s_w[wave][k];
-#pragma unroll
-      for (int j = 0; j < NV; ++j) A[j] = fmaf(src[int64_t(k) * step + 64 * j], wk, A[j]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float L = 0.f;
+  for (int p = threadIdx.x; p < np; p += 256) {
+    const int64_t r = row0 + p * pstride;
+    const float wgt = dsp_exp2(ws_ml[2 * r] - Mu);
+    s_w[p] = wgt;
+    L = fmaf(ws_ml[2 * r + 1], wgt, L);
   }
 #pragma unroll
   for (int mask = 1; mask < 64; mask <<= 1) L += dsp_shfl_xor(L, mask);
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  if (act) {
+  __syncthreads();  // s_red (max) read by all; s_w complete
+  if (lane == 0) s_red[wave] = L;
+  // weighted sum of the accumulators: wave w takes pieces w, w + 4, ...
+  const bool act = lane < D;
+  const float* src = ws_acc + row0 * D + (act ? lane : 0);
+  const int64_t step = pstride * D;
+  float A[NV];
 #pragma unroll
-    for (int j = 0; j < NV; ++j) o[lane + 64 * j] = narrow<Tag>(A[j] * inv);
+  for (int j = 0; j < NV; ++j) A[j] = 0.f;
+  int p = wave;
+  for (; p + 4 * (kInFlight - 1) < np; p += 4 * kInFlight) {
+    float v[kInFlight][NV];
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) v[u][j] = src[int64_t(p + 4 * u) * step + 64 * j];
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u) {
+      const float wk = s_w[p + 4 * u];
+#pragma unroll
+      for (int j = 0; j < NV; ++j) A[j] = fmaf(v[u][j], wk, A[j]);
+    }
+  }
+  for (; p < np; p += 4) {
+    const float wk = s_w[p];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) A[j] = fmaf(src[int64_t(p) * step + 64 * j], wk, A[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s_acc[wave][lane + 64 * j] = A[j];
+  __syncthreads();
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    const float Lt = s_red[0] + s_red[1] + s_red[2] + s_red[3];
+    const float At = s_acc[0][d] + s_acc[1][d] + s_acc[2][d] + s_acc[3][d];
+    o[d] = narrow<Tag>(At * (Lt > 0.f ? 1.f / Lt : 0.f));
   }
 }
 
@@ -513,7 +519,7 @@ int launch_balanced_hg(int W, const uint16_t* q, int64_t qsb, int64_t qsh, const
   const int st = dsp_launch_status();
   if (st != DSP_OK) return st;
   const int Hq = KVH * G;
-  decode_balanced_combine_kernel<Tag, D><<<dim3((Hq + 3) / 4, B), 256, 0, s>>>(
+  decode_balanced_combine_kernel<Tag, D><<<dim3(Hq, B), 256, 0, s>>>(
       ws_acc, ws_ml, ctx_lens, B, KVH, G, max_ctx, Wg, HG, out, osb, osh, err_count);
   return dsp_launch_status();
 }
@@ -577,6 +583,8 @@ int balanced_head_group(int32_t KVH) {
 bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
                              int32_t block_size) {
   if (B < 1 || B > kMaxBatch || KVH < 1 || max_ctx < 1) return false;
+  // the merge keeps one weight per worker in LDS
+  if (int64_t(device_cus()) * 4 * kOcc > kCombineMaxPieces) return false;
   if (block_size < (1 << kLog2Unit)) return false;
   if (D != 32 && D != 64 && D != 128) return false;
   // w * C stays far inside int64 for every worker index w
