@@ -471,9 +471,11 @@ def bench_c4(torch) -> dict:
     """Qwen3-1.7B shape (28 L, Hq 16, KVH 8, D 128): 32 sequences share a 2050-token
     prefix, fork it copy-on-write (the partial block is copied per sequence), append
     suffixes ~U[64, 512], run a 5-query causal verify over the paged cache (with the shared
-    prompt blocks attended once for the batch, and per sequence for comparison), then evict
-    10% of the live blocks by copying them into a spill pool."""
-    from dispec_amd.engine.hip_attn import paged_mq_attention
+    prompt blocks attended once for the batch, and per sequence for comparison) and a
+    one-query decode step the same two ways, then evict 10% of the live blocks by copying
+    them into a spill pool."""
+    from dispec_amd.engine.hip_attn import (decode_workspace, paged_decode_attention_blocks,
+                                           paged_mq_attention)
     from dispec_amd.kv.paged_cache import PagedKVCache
 
     L, Hq, KVH, D, bs, S, prefix, K = 28, 16, 8, 128, 16, 32, 2050, 5
@@ -532,6 +534,26 @@ def bench_c4(torch) -> dict:
 
     ver_s = _time_gpu(torch, lambda: verify(shared_tokens), 10) / L
     plain_s = _time_gpu(torch, lambda: verify(0), 10) / L
+
+    # a decode step of the forks (one query row each): shared-prefix multi-query kernel,
+    # as ModelRunner routes it, against the per-sequence decode kernel
+    cu1 = torch.arange(S + 1, dtype=torch.int32, device=dev)
+    q1, out1 = q[:, :S], out[:, :S]
+    ws1 = decode_workspace(S, Hq, KVH, D, max_ctx, dev)
+
+    def decode(sp):
+        for layer in range(L):
+            if sp:
+                paged_mq_attention(q1[layer], cache.key[layer], cache.value[layer], bt, cu1,
+                                   ctx_t, Hq // KVH, block_size=bs, max_q_len=1,
+                                   max_ctx=max_ctx, out=out1[layer], shared_prefix_tokens=sp)
+            else:
+                paged_decode_attention_blocks(q1[layer], cache.key[layer], cache.value[layer],
+                                              bt, ctx_t, Hq // KVH, block_size=bs,
+                                              max_ctx=max_ctx, out=out1[layer], workspace=ws1)
+
+    dec_s = _time_gpu(torch, lambda: decode(shared_tokens), 10) / L
+    dec_plain_s = _time_gpu(torch, lambda: decode(0), 10) / L
     shared = (prefix // bs) * bs          # full prefix blocks, read by every sequence
     unique_tokens = shared + sum(c - shared for c in ctx)
     logical_tokens = sum(ctx)
@@ -555,6 +577,8 @@ def bench_c4(torch) -> dict:
         "c4_verify_unique_GBps": unique_tokens * KVH * D * 4 / ver_s / 1e9,
         "c4_verify_logical_GBps": logical_tokens * KVH * D * 4 / ver_s / 1e9,
         "c4_verify_TFLOPs": flops / ver_s / 1e12,
+        "c4_fork_decode_us_per_layer": dec_s * 1e6,
+        "c4_fork_decode_plain_us_per_layer": dec_plain_s * 1e6,
         "c4_evict_blocks": nev, "c4_evict_us": ev_s * 1e6,
         "c4_evict_GBps": 2 * 2 * L * nev * cache.block_bytes / ev_s / 1e9,
     }

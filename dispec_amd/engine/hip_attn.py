@@ -116,6 +116,23 @@ def decode_workspace(batch, num_heads, num_kv_heads, head_dim, max_ctx, device):
     return torch.empty(need // 4 + 1, dtype=torch.float32, device=device) if need else None
 
 
+def mq_workspace(batch, num_heads, num_kv_heads, head_dim, max_q_len, max_ctx, device,
+                 shared_prefix_tokens=0):
+    """A float32 split-K workspace for every `paged_mq_attention` launch of this shape with
+    the automatic partition, or None when it needs none.  One buffer serves all layers of a
+    forward: the launches run in stream order."""
+    L = _lib.lib()
+    if shared_prefix_tokens:
+        P = L.dsp_paged_mq_shared_prefix_partition_tokens(
+            batch, num_heads, num_kv_heads, head_dim, max_q_len, max_ctx, shared_prefix_tokens)
+    else:
+        P = L.dsp_paged_mq_partition_tokens(batch, num_heads, num_kv_heads, head_dim,
+                                            max_q_len, max_ctx)
+    need = L.dsp_paged_mq_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, max_q_len,
+                                          max_ctx, P)
+    return torch.empty(need // 4 + 1, dtype=torch.float32, device=device) if need else None
+
+
 def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_groups,
                        block_size=16, scale=None, max_q_len=None, max_ctx=None, out=None,
                        err=None, partition_tokens=0, workspace=None, shared_prefix_tokens=0):

@@ -31,7 +31,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from dispec_amd.engine.hip_attn import (decode_workspace, paged_decode_attention_blocks,
+from dispec_amd.engine.hip_attn import (decode_workspace, mq_workspace,
+                                       paged_decode_attention_blocks,
                                         paged_mq_attention)
 from dispec_amd.engine.hip_prologue import qk_norm_rope_append
 from dispec_amd.kv.paged_cache import PagedKVCache
@@ -135,8 +136,8 @@ class ModelRunner:
                     torch.tensor(m.block_ids, dtype=torch.int32)
         dev = host.to(cache.key.device)                 # one H2D copy for all metadata
         decode = all(m.q_len == 1 for m in seq_meta)
-        shared = 0 if decode else self._shared_prefix(seq_meta, host[2 * B + 1:].view(B, width),
-                                                      cache.block_size)
+        shared = self._shared_prefix(seq_meta, host[2 * B + 1:].view(B, width),
+                                     cache.block_size)
         return _Batch(block_table=dev[2 * B + 1:].view(B, width), ctx_lens=dev[:B],
                       cu_q=dev[B:2 * B + 1], max_q_len=max(m.q_len for m in seq_meta),
                       max_ctx=width * cache.block_size, decode=decode, shared_prefix=shared)
@@ -175,7 +176,7 @@ class ModelRunner:
         q = qk_norm_rope_append(q, k, v, cos, sin, write_slots, cache, layer_idx,
                                 attn.q_norm if self.qk_norm else None,
                                 attn.k_norm if self.qk_norm else None)
-        if batch.decode:
+        if batch.decode and not batch.shared_prefix:
             o = paged_decode_attention_blocks(
                 q, cache.key[layer_idx], cache.value[layer_idx], batch.block_table,
                 batch.ctx_lens, self.kv_groups, block_size=cache.block_size, scale=self.scale,
@@ -184,7 +185,7 @@ class ModelRunner:
             o = paged_mq_attention(
                 q, cache.key[layer_idx], cache.value[layer_idx], batch.block_table, batch.cu_q,
                 batch.ctx_lens, self.kv_groups, block_size=cache.block_size, scale=self.scale,
-                max_q_len=batch.max_q_len, max_ctx=batch.max_ctx,
+                max_q_len=batch.max_q_len, max_ctx=batch.max_ctx, workspace=batch.workspace,
                 shared_prefix_tokens=batch.shared_prefix)
         return attn.o_proj(o.reshape(T, self.num_heads * self.head_dim))
 
@@ -200,14 +201,22 @@ class ModelRunner:
                   write_slots: torch.Tensor, batch: _Batch, cache: PagedKVCache) -> torch.Tensor:
         """The layer loop of `forward` over batch metadata already on the device.
 
-        No host sync and, for a decode batch that brings its own workspace, no allocation
-        outside torch's allocator: this is the body a HIP graph captures."""
+        No host sync and, for a batch that brings its own workspace, no allocation outside
+        torch's allocator: this is the body a HIP graph captures.  Decode batches whose
+        sequences share leading blocks (copy-on-write forks) take the shared-prefix
+        multi-query kernel, which reads those blocks once for the batch."""
         cos, sin = self.rope(positions)
         x = self.embed(token_ids)
-        if batch.decode and batch.workspace is None:
-            batch.workspace = decode_workspace(
-                batch.ctx_lens.shape[0], self.num_heads, self.num_kv_heads, self.head_dim,
-                batch.max_ctx, cache.key.device)
+        if batch.workspace is None:
+            B = batch.ctx_lens.shape[0]
+            if batch.decode and not batch.shared_prefix:
+                batch.workspace = decode_workspace(B, self.num_heads, self.num_kv_heads,
+                                                   self.head_dim, batch.max_ctx,
+                                                   cache.key.device)
+            else:
+                batch.workspace = mq_workspace(B, self.num_heads, self.num_kv_heads,
+                                               self.head_dim, batch.max_q_len, batch.max_ctx,
+                                               cache.key.device, batch.shared_prefix)
         for i, layer in enumerate(self.layers):
             h = layer.input_layernorm(x)
             x = x + self._attention(layer, h, cos, sin, write_slots, cache, i, batch)

@@ -139,6 +139,33 @@ def test_verify_of_forked_sequences_uses_the_shared_prefix():
     assert both.runner._batch(meta, both.cache).shared_prefix == 640
 
 
+def test_decode_of_forked_sequences_uses_the_shared_prefix():
+    """Decode steps of five copy-on-write forks of one 640-token prompt: each step is a
+    q_len 1 batch whose 40 leading blocks are shared, which the runner attends once for the
+    batch instead of the per-sequence decode kernel.  Twenty steps cross a block boundary
+    of the private suffixes; logits match the native path at every step."""
+    from dispec_amd.engine.model_runner import SeqMeta
+    gm, cm = _pair("qwen3")
+    both = _Both(gm, cm, num_blocks=96)
+    g = torch.Generator().manual_seed(13)
+    prompt = torch.randint(0, 128, (640,), generator=g).tolist()
+    got, ref = both.forward([(0, prompt, 0)])
+    for child in range(1, 5):
+        both.cache.manager.cow_fork(0, child)
+    toks = torch.randint(0, 128, (5,), generator=g).tolist()   # diverging first tokens
+    cur = 640
+    mgr = both.cache.manager
+    for step in range(20):
+        got, ref = both.forward([(sid, [toks[sid]], cur) for sid in range(5)])
+        c = _cos(got, ref).min().item()
+        assert c >= 0.999, f"step {step}, ctx {cur + 1}: cosine {c:.5f}"
+        meta = [SeqMeta(list(mgr.block_table(s).block_ids), 1, cur + 1) for s in range(5)]
+        batch = both.runner._batch(meta, both.cache)
+        assert batch.decode and batch.shared_prefix == 640
+        toks = ref.argmax(-1).tolist()
+        cur += 1
+
+
 def test_rejects_other_backends():
     from dispec_amd.engine.model_runner import ModelRunner
     with pytest.raises(ValueError, match="hip"):

@@ -32,6 +32,8 @@ def test_forks_of_one_prompt():
     # config 4: 2050-token prompt, 128 full blocks shared, private partial block
     tables = _forks(8, 128, 3)
     assert _detect(tables, [5] * 8, [2050 + 40 + 5] * 8) == 2048
+    # their decode steps (q_len 1) as well
+    assert _detect(tables, [1] * 8, [2050 + 41] * 8) == 2048
 
 
 def test_rounded_down_to_128_and_limited_by_the_queries():
