@@ -791,8 +791,9 @@ def bench_copy(torch) -> dict:
 
 def bench_copy_ceiling(torch) -> dict:
     """The ceiling of the byte-moving kernels on this GPU: a 2 GiB streaming copy
-    (dsp_probe_stream_copy, non-temporal loads and stores), best of three grid sizes,
-    read + write bytes over time."""
+    (dsp_probe_stream_copy, non-temporal loads and stores), best of three grid sizes --
+    64, 16 and 4 KiB per workgroup, the last two one-shot workgroups -- read + write bytes
+    over time."""
     from dispec_amd import _lib
     lib = _lib.lib()
     n = 2 << 30
@@ -801,7 +802,7 @@ def bench_copy_ceiling(torch) -> dict:
     src.fill_(7)
     stream = torch.cuda.current_stream().cuda_stream
     best = None
-    for wgs in (2048, 8192, 32768):
+    for wgs in (32768, 131072, 524288):
         def f():
             _lib.check(lib.dsp_probe_stream_copy(src.data_ptr(), dst.data_ptr(), n, wgs, stream),
                        "probe")

@@ -156,6 +156,44 @@ def test_ensure_writable_unshares_a_refcount_fork(hip):
     assert np.array_equal(bits(c.key), kp)
 
 
+@pytest.mark.parametrize("bs,H,D,dtype", [(32, 3, 40, torch.bfloat16),   # 7680 B blocks
+                                          (16, 3, 5, torch.float16),     # 30 B rows
+                                          (64, 8, 128, torch.bfloat16),  # 128 KiB blocks
+                                          (16, 1, 8, torch.float32)])    # 512 B blocks
+def test_copies_split_into_pieces(hip, bs, H, D, dtype):
+    """The block copy and the transport kernels move a block in 4 KiB pieces (one
+    workgroup each): blocks that are not a multiple of a piece, smaller than one, many
+    pieces long, and rows that need narrower vectors."""
+    L = 3
+    lens = [5 * bs + 3, bs, 1, 2 * bs - 1]
+    NB = sum(-(-n // bs) for n in lens) + 12
+    c = _cache(L, NB, bs, H, D, dtype=dtype, seed=110 + bs + D)
+    tables = random_block_tables(NB, lens, bs, 111)
+    kp, vp = bits(c.key), bits(c.value)
+    kbuf, vbuf, cu = c.export_batch(list(zip(tables, lens)))
+    for b, (ids, n) in enumerate(zip(tables, lens)):
+        rows = slice(L * cu[b], L * cu[b + 1])
+        shape = (L, n, H, D)
+        assert np.array_equal(bits(kbuf)[rows].reshape(shape), ref_cpu.export_contiguous(kp, ids, n, bs))
+        assert np.array_equal(bits(vbuf)[rows].reshape(shape), ref_cpu.export_contiguous(vp, ids, n, bs))
+    used = {b for t in tables for b in t}
+    free = [b for b in range(NB) if b not in used]
+    pairs = list(zip(tables[0][:4], free[:4]))
+    c.copy_blocks_from(c, [p[0] for p in pairs], [p[1] for p in pairs])
+    ref_cpu.copy_blocks(kp, kp, pairs, bs)
+    ref_cpu.copy_blocks(vp, vp, pairs, bs)
+    assert np.array_equal(bits(c.key), kp) and np.array_equal(bits(c.value), vp)
+    # import sequence 0's payload into sequence 3's blocks (its first 2*bs - 1 tokens)
+    n3 = lens[3]
+    k0 = kbuf[:L * lens[0]].view(L, lens[0], H, D)[:, :n3].contiguous()
+    v0 = vbuf[:L * lens[0]].view(L, lens[0], H, D)[:, :n3].contiguous()
+    c.import_contiguous(tables[3], k0, v0)
+    ref_cpu.import_contiguous(kp, tables[3], bits(k0), bs)
+    ref_cpu.import_contiguous(vp, tables[3], bits(v0), bs)
+    assert np.array_equal(bits(c.key), kp) and np.array_equal(bits(c.value), vp)
+    c.check_errors()
+
+
 def test_copy_blocks_out_of_range_is_reported(hip):
     from dispec_amd.kv.paged_cache import PagedKVCache
     c = _cache(2, 8, 16, 2, 64, seed=100)
