@@ -66,6 +66,20 @@ __device__ __forceinline__ void load_bias4(const uint16_t* __restrict__ bias, in
   }
 }
 
+// Bias and activation of one output, in the order the reference rounds (see the header
+// comment); the result is a bf16 value held in a float.  Accumulation into C comes after.
+__device__ __forceinline__ float epi_bias_act(float y, float b, int32_t bias_mode, int32_t act) {
+  if (bias_mode == 1) {
+    y = bf16_round(bf16_round(y) + b);
+  } else if (bias_mode == 2) {
+    y = bf16_round(y + b);
+  } else {
+    y = bf16_round(y);
+  }
+  if (act == 1) y = bf16_round(0.5f * y * (1.f + erff(y * 0.70710678118654752f)));
+  return y;
+}
+
 // Epilogue of four consecutive outputs (row crow, columns nb..nb+3, clipped at N) in the
 // order the reference rounds (see the header comment); b4 is their bias (bias_mode != 0).
 __device__ __forceinline__ void store_c4(const f32x4& v, uint16_t* __restrict__ crow, int64_t nb,
@@ -91,15 +105,7 @@ __device__ __forceinline__ void store_c4(const f32x4& v, uint16_t* __restrict__ 
   uint16_t ybits[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    float y = v[e];
-    if (bias_mode == 1) {
-      y = bf16_round(bf16_round(y) + b4[e]);
-    } else if (bias_mode == 2) {
-      y = bf16_round(y + b4[e]);
-    } else {
-      y = bf16_round(y);
-    }
-    if (act == 1) y = bf16_round(0.5f * y * (1.f + erff(y * 0.70710678118654752f)));
+    float y = epi_bias_act(v[e], b4[e], bias_mode, act);
     if (accumulate) y = bf16_round(dsp_bf16lo(old[e]) + y);
     ybits[e] = dsp_f32_to_bf16(y);
   }
@@ -360,20 +366,70 @@ __global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  // acc[i][j] is a C^T tile: lane holds columns n = wn + 16j + 4*(lane/16) + e of row
-  // m = wm + 16i + lane%16.
+  // Epilogue through LDS.  acc[i][j] is a C^T tile: lane holds columns
+  // n = wn + 16j + 4*(lane/16) + e of row m = wm + 16i + lane%16, so stores straight from
+  // it write 16 rows x 32 bytes per instruction.  Instead each wave rounds its 64 x 128
+  // outputs into its own 16 KiB of the (now idle) stage buffers as bf16 rows of 256 bytes
+  // (16-byte chunk c of row r at slot c ^ (r & 15): conflict-free both ways) and reads them
+  // back four whole rows per instruction, so C is written in full 256-byte row runs with
+  // 16-byte lanes -- half the store instructions, every cache line written whole.
+  static_assert(big::kNW * big::kTM * big::kTN * 2 <= 2 * big::kStageB, "C tile fits the stages");
   float b4[big::kFN][4] = {};
   if (kBias) {
 #pragma unroll
     for (int j = 0; j < big::kFN; ++j) load_bias4(bias, n0 + wn + 16 * j + 4 * fq, N, b4[j]);
   }
+  __syncthreads();   // every wave is done reading the last stage
+  char* ct = lds + wave * (big::kTM * big::kTN * 2);
 #pragma unroll
   for (int i = 0; i < big::kFM; ++i) {
-    const int64_t m = m0 + wm + 16 * i + fr;
-    if (m >= M) continue;
+    const int r = 16 * i + fr;
 #pragma unroll
-    for (int j = 0; j < big::kFN; ++j)
-      store_c4(acc[i][j], c + m * ldc, n0 + wn + 16 * j + 4 * fq, N, b4[j], kBias, kAct, kAccum);
+    for (int j = 0; j < big::kFN; ++j) {
+      uint16_t yb[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        yb[e] = dsp_f32_to_bf16(epi_bias_act(acc[i][j][e], b4[j][e], kBias, kAct));
+      const int col = 16 * j + 4 * fq;
+      *reinterpret_cast<dsp_u32x2*>(ct + r * (big::kTN * 2) + (((col >> 3) ^ (r & 15)) * 16) +
+                                    (col & 7) * 2) =
+          dsp_u32x2{uint32_t(yb[0]) | (uint32_t(yb[1]) << 16),
+                    uint32_t(yb[2]) | (uint32_t(yb[3]) << 16)};
+    }
+  }
+  const int cl = lane & 15;
+  const int64_t n = n0 + wn + 8 * cl;
+  const bool vec_c = n + 7 < N;
+#pragma unroll
+  for (int q = 0; q < big::kTM / 4; ++q) {
+    const int r = 4 * q + (lane >> 4);
+    const dsp_u32x4 v =
+        *reinterpret_cast<const dsp_u32x4*>(ct + r * (big::kTN * 2) + ((cl ^ (r & 15)) * 16));
+    const int64_t m = m0 + wm + r;
+    if (m >= M) continue;
+    uint16_t* dst = c + m * ldc + n;
+    if (vec_c && dsp_aligned(dst, 16)) {
+      dsp_u32x4 w = v;
+      if (kAccum) {
+        const dsp_u32x4 old = *reinterpret_cast<const dsp_u32x4*>(dst);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint16_t lo = dsp_f32_to_bf16(bf16_round(dsp_bf16lo(old[e]) + dsp_bf16lo(v[e])));
+          const uint16_t hi = dsp_f32_to_bf16(bf16_round(dsp_bf16hi(old[e]) + dsp_bf16hi(v[e])));
+          w[e] = uint32_t(lo) | (uint32_t(hi) << 16);
+        }
+      }
+      *reinterpret_cast<dsp_u32x4*>(dst) = w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (n + e >= N) break;
+        const uint32_t word = v[e >> 1];
+        uint16_t y = uint16_t((e & 1) ? word >> 16 : word);
+        if (kAccum) y = dsp_f32_to_bf16(bf16_round(dsp_bf16lo(dst[e]) + dsp_bf16lo(y)));
+        dst[e] = y;
+      }
+    }
   }
 }
 

@@ -203,6 +203,7 @@ def test_escalation_export_map_import_round_trip():
     (4, 2053, 1000, 2, 1, False),   # F.linear + gelu (residual down projection)
     (4, 2053, 1000, 0, 0, True),    # no bias, accumulate (residual up projection)
     (40, 100, 1024, 2, 1, True),    # 160 tiles of mostly clamped rows
+    (4, 2053, 996, 0, 0, True),     # N % 8 = 4 and 1992-byte rows: C chunks partial, unaligned
 ])
 def test_large_tile_gemm_path(B, M, N, bias_mode, act, accum):
     """Problems of >= 128 output tiles of 256 x 256 take the direct-to-LDS kernel.  A design
