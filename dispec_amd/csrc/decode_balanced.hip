@@ -394,11 +394,11 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
 
 // One workgroup (4 waves) per (sequence b, query head h).  Merges the pieces of segment
 // (b, h / G) when more than one worker covered it, writes zeros for an empty context, and
-// counts a context length outside [0, max_ctx] once per sequence.  A long context among
-// short ones spans hundreds of workers, so the pieces are split over the 4 waves, each
-// lane keeping 16 piece rows in flight; the waves' sums meet in LDS.
-constexpr int kCombineMaxPieces = 4 * kOcc * 1024;  // workers of a launch: <= 4 x kOcc x CUs
-
+// counts a context length outside [0, max_ctx] once per sequence.  One pass with online
+// rescaling: wave w takes pieces w, w + 4, ..., each lane loading the (max, sum) pair and
+// its dims of the accumulator of 16 pieces at once, so the merge costs two dependent
+// memory round trips (ctx_lens, then the pieces) whatever the piece count; the waves'
+// partial merges meet in LDS.
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
@@ -406,10 +406,9 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
     int32_t num_workers, int32_t HG, uint16_t* __restrict__ out, int64_t osb, int64_t osh,
     int32_t* __restrict__ err_count) {
   constexpr int NV = D > 64 ? 2 : 1;  // dims per lane: lane, lane + 64
-  constexpr int kInFlight = 16;       // piece rows loaded per lane before their FMAs
-  __shared__ float s_w[kCombineMaxPieces];
+  constexpr int kInFlight = 16;       // pieces loaded per lane before they are folded in
   __shared__ float s_acc[4][NV * 64];
-  __shared__ float s_red[4];
+  __shared__ float s_ml[4][2];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h = blockIdx.x, b = blockIdx.y;
   int64_t total = 0, pre = 0;
@@ -439,60 +438,60 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
   // piece p is slot (b*NG + kvg) + w0 + p; its head hw, row g
   const int64_t row0 = ((int64_t(b) * NG + kvg + w0) * HG + hw) * G + g;
   const int64_t pstride = int64_t(HG) * G;  // rows between consecutive slots
-
-  // row max over the pieces, then their weights 2^(m_p - M) and the weighted row sum
-  float M = -INFINITY;
-  for (int p = threadIdx.x; p < np; p += 256) M = fmaxf(M, ws_ml[2 * (row0 + p * pstride)]);
-#pragma unroll
-  for (int mask = 1; mask < 64; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
-  if (lane == 0) s_red[wave] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  const float Mu = M == -INFINITY ? 0.f : M;
-  float L = 0.f;
-  for (int p = threadIdx.x; p < np; p += 256) {
-    const int64_t r = row0 + p * pstride;
-    const float wgt = dsp_exp2(ws_ml[2 * r] - Mu);
-    s_w[p] = wgt;
-    L = fmaf(ws_ml[2 * r + 1], wgt, L);
-  }
-#pragma unroll
-  for (int mask = 1; mask < 64; mask <<= 1) L += dsp_shfl_xor(L, mask);
-  __syncthreads();  // s_red (max) read by all; s_w complete
-  if (lane == 0) s_red[wave] = L;
-  // weighted sum of the accumulators: wave w takes pieces w, w + 4, ...
   const bool act = lane < D;
   const float* src = ws_acc + row0 * D + (act ? lane : 0);
-  const int64_t step = pstride * D;
-  float A[NV];
+  const float* ml = ws_ml + 2 * row0;
+
+  float Mw = -INFINITY, Lw = 0.f, A[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) A[j] = 0.f;
-  int p = wave;
-  for (; p + 4 * (kInFlight - 1) < np; p += 4 * kInFlight) {
-    float v[kInFlight][NV];
-#pragma unroll
-    for (int u = 0; u < kInFlight; ++u)
-#pragma unroll
-      for (int j = 0; j < NV; ++j) v[u][j] = src[int64_t(p + 4 * u) * step + 64 * j];
+  for (int p = wave; p < np; p += 4 * kInFlight) {
+    float mv[kInFlight], lv[kInFlight], v[kInFlight][NV];
 #pragma unroll
     for (int u = 0; u < kInFlight; ++u) {
-      const float wk = s_w[p + 4 * u];
+      const int pp = p + 4 * u;
+      const bool in = pp < np;
+      const int64_t r = in ? int64_t(pp) * pstride : 0;
+      mv[u] = in ? ml[2 * r] : -INFINITY;
+      lv[u] = in ? ml[2 * r + 1] : 0.f;
+#pragma unroll
+      for (int j = 0; j < NV; ++j) v[u][j] = in ? src[r * D + 64 * j] : 0.f;
+    }
+    float bm = Mw;
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u) bm = fmaxf(bm, mv[u]);
+    const float bmu = bm == -INFINITY ? 0.f : bm;
+    const float keep = dsp_exp2(Mw - bmu);
+    Lw *= keep;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) A[j] *= keep;
+#pragma unroll
+    for (int u = 0; u < kInFlight; ++u) {
+      const float wk = dsp_exp2(mv[u] - bmu);
+      Lw = fmaf(lv[u], wk, Lw);
 #pragma unroll
       for (int j = 0; j < NV; ++j) A[j] = fmaf(v[u][j], wk, A[j]);
     }
+    Mw = bm;
   }
-  for (; p < np; p += 4) {
-    const float wk = s_w[p];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) A[j] = fmaf(src[int64_t(p) * step + 64 * j], wk, A[j]);
+  if (lane == 0) {
+    s_ml[wave][0] = Mw;
+    s_ml[wave][1] = Lw;
   }
 #pragma unroll
   for (int j = 0; j < NV; ++j) s_acc[wave][lane + 64 * j] = A[j];
   __syncthreads();
   if (threadIdx.x < D) {
     const int d = threadIdx.x;
-    const float Lt = s_red[0] + s_red[1] + s_red[2] + s_red[3];
-    const float At = s_acc[0][d] + s_acc[1][d] + s_acc[2][d] + s_acc[3][d];
+    const float M = fmaxf(fmaxf(s_ml[0][0], s_ml[1][0]), fmaxf(s_ml[2][0], s_ml[3][0]));
+    const float Mu = M == -INFINITY ? 0.f : M;
+    float Lt = 0.f, At = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float wk = dsp_exp2(s_ml[w][0] - Mu);
+      Lt = fmaf(s_ml[w][1], wk, Lt);
+      At = fmaf(s_acc[w][d], wk, At);
+    }
     o[d] = narrow<Tag>(At * (Lt > 0.f ? 1.f / Lt : 0.f));
   }
 }
@@ -583,8 +582,6 @@ int balanced_head_group(int32_t KVH) {
 bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
                              int32_t block_size) {
   if (B < 1 || B > kMaxBatch || KVH < 1 || max_ctx < 1) return false;
-  // the merge keeps one weight per worker in LDS
-  if (int64_t(device_cus()) * 4 * kOcc > kCombineMaxPieces) return false;
   if (block_size < (1 << kLog2Unit)) return false;
   if (D != 32 && D != 64 && D != 128) return false;
   // w * C stays far inside int64 for every worker index w
