@@ -365,6 +365,53 @@ def bench_skew(torch) -> dict:
             res[f"{name}_{label}_GBps"] = kv_bytes / us / 1e3
         del kc, vc
         torch.cuda.empty_cache()
+    res.update(_verify_skew(torch))
+    return res
+
+
+def _verify_skew(torch) -> dict:
+    """A 5-query verify (Qwen3-1.7B heads: Hq 16, KVH 8, D 128) over one 32768-token context
+    beside 15 of 512: the balanced split-K kernel (what ModelRunner picks for such a batch)
+    against the fixed key partitions the library sizes from max_ctx."""
+    from dispec_amd import _lib
+    from dispec_amd.engine.hip_attn import paged_mq_attention
+
+    dev, Hq, KVH, D, bs, ql = "cuda", 16, 8, 128, 16, 5
+    ctxs = [32768] + [512] * 15
+    B = len(ctxs)
+    need = [-(-c // bs) for c in ctxs]
+    NB = int(sum(need) * 1.25) + 8
+    kc = torch.empty((NB * bs, KVH, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.empty_like(kc)
+    _fill_randn(torch, kc.view(1, -1), 4005)
+    _fill_randn(torch, vc.view(1, -1), 4006)
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(4007)).tolist()
+    bt = torch.zeros((B, max(need)), dtype=torch.int32)
+    at = 0
+    for i, n in enumerate(need):
+        bt[i, :n] = torch.tensor(perm[at:at + n])
+        at += n
+    bt = bt.to(dev)
+    ctx = torch.tensor(ctxs, dtype=torch.int32, device=dev)
+    cu = torch.arange(0, (B + 1) * ql, ql, dtype=torch.int32, device=dev)
+    q = torch.randn((B * ql, Hq, D), generator=torch.Generator(device=dev).manual_seed(4008),
+                    device=dev).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    lib = _lib.lib()
+    wsb = max(lib.dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, ql, max(ctxs), p)
+              for p in (0, _lib.DSP_SPLIT_BALANCED))
+    ws = torch.empty(wsb // 4 + 1, dtype=torch.float32, device=dev)
+    kv_bytes = sum(ctxs) * KVH * D * 2 * 2
+    res = {}
+    for label, bal in (("balanced", True), ("partitioned", False)):
+        def f():
+            paged_mq_attention(q, kc, vc, bt, cu, ctx, Hq // KVH, block_size=bs, max_q_len=ql,
+                               max_ctx=max(ctxs), out=out, workspace=ws, balanced=bal)
+        us = _time_gpu(torch, f, 20) * 1e6
+        res[f"verify_skew_{label}_us"] = us
+        res[f"verify_skew_{label}_GBps"] = kv_bytes / us / 1e3
+    del kc, vc
+    torch.cuda.empty_cache()
     return res
 
 

@@ -20,6 +20,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libdispec_hip.so"
 
 DSP_BF16, DSP_F16, DSP_F32 = 0, 1, 2
 DSP_OK, DSP_EINVAL, DSP_EALIGN, DSP_EUNSUPPORTED, DSP_EWORKSPACE = 0, -1, -2, -3, -4
+DSP_SPLIT_BALANCED = -1   # partition_tokens of dsp_paged_mq_attention: balanced split-K
 
 # (name, restype, argtypes) for every symbol the header declares.
 _P = c_void_p

@@ -76,13 +76,25 @@ __device__ __forceinline__ int wave_sum(int v) {
   return __builtin_amdgcn_readfirstlane(v);
 }
 
+// Work units of sequence b.  Decode (cu_q null): its clamped context.  Multi-query: none
+// for an empty query block or a context outside [q_len, max_ctx] (the merge kernel writes
+// such a sequence's rows as zeros and counts it), else its context.
+__device__ __forceinline__ int seq_units(const int32_t* __restrict__ ctx_lens,
+                                         const int32_t* __restrict__ cu_q, int b, int max_ctx) {
+  const int ctx = ctx_lens[b];
+  if (cu_q == nullptr) return units_of(ctx, max_ctx);
+  const int ql = cu_q[b + 1] - cu_q[b];
+  return (ql <= 0 || ctx < ql || ctx > max_ctx) ? 0 : units_of(ctx, max_ctx);
+}
+
 // Units of one KV head summed over all sequences (the whole launch is KVH times this).
-__device__ __forceinline__ int64_t head_units(const int32_t* __restrict__ ctx_lens, int B,
+__device__ __forceinline__ int64_t head_units(const int32_t* __restrict__ ctx_lens,
+                                              const int32_t* __restrict__ cu_q, int B,
                                               int max_ctx) {
   int64_t t = 0;
   for (int b0 = 0; b0 < B; b0 += 64) {
     const int b = b0 + __lane_id();
-    t += wave_sum(b < B ? units_of(ctx_lens[b], max_ctx) : 0);
+    t += wave_sum(b < B ? seq_units(ctx_lens, cu_q, b, max_ctx) : 0);
   }
   return t;
 }
@@ -106,8 +118,9 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
     const uint16_t* __restrict__ q, int64_t qsb, int64_t qsh, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
     const int32_t* __restrict__ bt, int64_t bt_stride, int32_t log2_bs,
-    const int32_t* __restrict__ ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t max_ctx,
-    float scale_log2, int32_t num_workers, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
+    const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ cu_q, int32_t B,
+    int32_t KVH, int32_t G, int32_t RPH, int32_t max_ctx, float scale_log2,
+    int32_t num_workers, float* __restrict__ ws_acc, float* __restrict__ ws_ml,
     uint16_t* __restrict__ out, int64_t osb, int64_t osh, int32_t* __restrict__ err_count) {
   constexpr int NKK = D / 32;       // 32-dim K steps of the score MFMA
   constexpr int NT = D / 16;        // 16-dim output tiles
@@ -121,12 +134,11 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
   const int lane = threadIdx.x & 63;
   const int hw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // head within the group
   const int NG = KVH / HG;                                          // head groups
-  const int n = lane & 15;   // packed row = query head kvh*G + n (MFMA N index)
+  const int n = lane & 15;   // packed row (MFMA N index): query qi = n / G, head g = n % G
   const int grp = lane >> 4; // lane group: K sub-range of the MFMA operands
-  const bool row_ok = n < G;
 
   // ---- this worker's unit range and where it starts
-  const int64_t C = head_units(ctx_lens, B, max_ctx) * NG;
+  const int64_t C = head_units(ctx_lens, cu_q, B, max_ctx) * NG;
   const int64_t W = active_workers(C, num_workers);
   const int64_t w = blockIdx.x;
   if (w >= W) return;
@@ -138,7 +150,7 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
     for (int b0 = 0; b0 < B; b0 += 64) {
       const int bb = b0 + lane;
       const int c = bb < B ? clamp_ctx(ctx_lens[bb], max_ctx) : 0;
-      const int v = (c + (1 << kLog2Unit) - 1) >> kLog2Unit;
+      const int v = bb < B ? seq_units(ctx_lens, cu_q, bb, max_ctx) : 0;
       const int incl = wave_incl_scan(v);
       const uint64_t hit = __ballot(int64_t(NG) * (base + incl) > U);
       if (hit) {
@@ -171,12 +183,19 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
     const int kvh = kvg * HG + hw;
     const int64_t bt_row = int64_t(b) * bt_stride;
     const int64_t head_off = int64_t(kvh) * kvs_head;
+    // query rows of sequence b: token q0 + qi, head kvh*G + g; row qi sees keys < lim
+    const int q0 = cu_q ? cu_q[b] : b;
+    const int ql = cu_q ? cu_q[b + 1] - q0 : 1;
+    const bool row_ok = n < ql * G;
+    const int qi = row_ok ? n / G : 0;
+    const int g = row_ok ? n - qi * G : 0;
+    const int lim = min(ke, ctx - ql + qi + 1);
 
     dsp_u32x4 qop[NKK];
 #pragma unroll
     for (int kk = 0; kk < NKK; ++kk)
-      qop[kk] = row_ok ? *reinterpret_cast<const dsp_u32x4*>(q + int64_t(b) * qsb +
-                                                             int64_t(kvh * G + n) * qsh + 32 * kk +
+      qop[kk] = row_ok ? *reinterpret_cast<const dsp_u32x4*>(q + int64_t(q0 + qi) * qsb +
+                                                             int64_t(kvh * G + g) * qsh + 32 * kk +
                                                              8 * grp)
                        : dsp_u32x4{0u, 0u, 0u, 0u};
 
@@ -289,7 +308,7 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int key = t0 + 16 * st + 4 * grp + j;
-          s[st][j] = (row_ok && key < ke) ? sc[st][j] * scale_log2 : -INFINITY;
+          s[st][j] = (row_ok && key < lim) ? sc[st][j] * scale_log2 : -INFINITY;
           mx = fmaxf(mx, s[st][j]);
         }
       }
@@ -356,14 +375,14 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
     if (row_ok) {
       if (whole) {
         const float inv = lpart > 0.f ? 1.f / lpart : 0.f;
-        uint16_t* o = out + int64_t(b) * osb + int64_t(kvh * G + n) * osh + 4 * grp;
+        uint16_t* o = out + int64_t(q0 + qi) * osb + int64_t(kvh * G + g) * osh + 4 * grp;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
           for (int j = 0; j < 4; ++j) o[16 * nt + j] = narrow<Tag>(acc[nt][j] * inv);
       } else {
         // piece (segment s = b*NG + kvg, worker w) is slot s + w; its head hw, row n
-        const int64_t row = ((int64_t(b) * NG + kvg + w) * HG + hw) * G + n;
+        const int64_t row = ((int64_t(b) * NG + kvg + w) * HG + hw) * RPH + n;
         float* a = ws_acc + row * D + 4 * grp;
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<f32x4*>(a + 16 * nt) = acc[nt];
@@ -384,7 +403,7 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
       do {
         if (++b >= B) break;
         ctx = clamp_ctx(ctx_lens[b], max_ctx);
-        nb = (ctx + (1 << kLog2Unit) - 1) >> kLog2Unit;
+        nb = seq_units(ctx_lens, cu_q, b, max_ctx);
       } while (nb == 0);
       if (b >= B) break;
     }
@@ -392,9 +411,11 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
   if (err_count && __ballot(any_bad) && lane == 0) atomicAdd(err_count, 1);
 }
 
-// One workgroup (4 waves) per (sequence b, query head h).  Merges the pieces of segment
-// (b, h / G) when more than one worker covered it, writes zeros for an empty context, and
-// counts a context length outside [0, max_ctx] once per sequence.  One pass with online
+// One workgroup (4 waves) per (sequence b, query head h, query i).  Merges the pieces of
+// segment (b, h / G) when more than one worker covered it, writes zeros for an empty
+// context, and counts a bad length once per sequence: for decode (cu_q null, one query per
+// sequence) a context outside [0, max_ctx]; for multi-query a context outside
+// [q_len, max_ctx], whose rows are written as zeros.  One pass with online
 // rescaling: wave w takes pieces w, w + 4, ..., each lane loading the (max, sum) pair and
 // its dims of the accumulator of 16 pieces at once, so the merge costs two dependent
 // memory round trips (ctx_lens, then the pieces) whatever the piece count; the waves'
@@ -402,27 +423,30 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
-    const int32_t* __restrict__ ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t max_ctx,
-    int32_t num_workers, int32_t HG, uint16_t* __restrict__ out, int64_t osb, int64_t osh,
-    int32_t* __restrict__ err_count) {
+    const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ cu_q, int32_t B,
+    int32_t KVH, int32_t G, int32_t RPH, int32_t max_ctx, int32_t num_workers, int32_t HG,
+    uint16_t* __restrict__ out, int64_t osb, int64_t osh, int32_t* __restrict__ err_count) {
   constexpr int NV = D > 64 ? 2 : 1;  // dims per lane: lane, lane + 64
   constexpr int kInFlight = 16;       // pieces loaded per lane before they are folded in
   __shared__ float s_acc[4][NV * 64];
   __shared__ float s_ml[4][2];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int h = blockIdx.x, b = blockIdx.y;
+  const int h = blockIdx.x, b = blockIdx.y, i = blockIdx.z;
+  const int q0 = cu_q ? cu_q[b] : b;
+  const int ql = cu_q ? cu_q[b + 1] - q0 : 1;
+  if (i >= ql) return;
   int64_t total = 0, pre = 0;
   for (int b0 = 0; b0 < B; b0 += 64) {
     const int bb = b0 + lane;
-    const int v = bb < B ? units_of(ctx_lens[bb], max_ctx) : 0;
+    const int v = bb < B ? seq_units(ctx_lens, cu_q, bb, max_ctx) : 0;
     total += wave_sum(v);
     pre += wave_sum(bb < b ? v : 0);
   }
   const int raw = ctx_lens[b];
-  if (h == 0 && threadIdx.x == 0 && err_count && (raw < 0 || raw > max_ctx))
-    atomicAdd(err_count, 1);
-  const int nb = units_of(raw, max_ctx);
-  uint16_t* o = out + int64_t(b) * osb + int64_t(h) * osh;
+  const bool bad = cu_q ? (raw < ql || raw > max_ctx) : (raw < 0 || raw > max_ctx);
+  if (h == 0 && i == 0 && threadIdx.x == 0 && err_count && bad) atomicAdd(err_count, 1);
+  const int nb = seq_units(ctx_lens, cu_q, b, max_ctx);
+  uint16_t* o = out + int64_t(q0 + i) * osb + int64_t(h) * osh;
   if (nb == 0) {
     if (threadIdx.x < D) o[threadIdx.x] = 0;
     return;
@@ -435,9 +459,9 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
   const int64_t w0 = ((cs + 1) * W - 1) / C, w1 = (ce * W - 1) / C;
   if (w0 == w1) return;  // one worker covered the segment and wrote the output
   const int np = static_cast<int>(w1 - w0 + 1);
-  // piece p is slot (b*NG + kvg) + w0 + p; its head hw, row g
-  const int64_t row0 = ((int64_t(b) * NG + kvg + w0) * HG + hw) * G + g;
-  const int64_t pstride = int64_t(HG) * G;  // rows between consecutive slots
+  // piece p is slot (b*NG + kvg) + w0 + p; its head hw, row i*G + g
+  const int64_t row0 = ((int64_t(b) * NG + kvg + w0) * HG + hw) * RPH + i * G + g;
+  const int64_t pstride = int64_t(HG) * RPH;  // rows between consecutive slots
   const bool act = lane < D;
   const float* src = ws_acc + row0 * D + (act ? lane : 0);
   const float* ml = ws_ml + 2 * row0;
@@ -500,26 +524,27 @@ template <typename Tag, int D, int HG>
 int launch_balanced_hg(int W, const uint16_t* q, int64_t qsb, int64_t qsh, const uint16_t* kc,
                        const uint16_t* vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
                        const int32_t* bt, int64_t bt_stride, int32_t log2_bs,
-                       const int32_t* ctx_lens, int32_t B, int32_t KVH, int32_t G,
-                       int32_t max_ctx, float scale_log2, float* ws_acc, float* ws_ml,
-                       uint16_t* out, int64_t osb, int64_t osh, int32_t* err_count,
-                       hipStream_t s) {
+                       const int32_t* ctx_lens, const int32_t* cu_q, int32_t max_q_len,
+                       int32_t B, int32_t KVH, int32_t G, int32_t max_ctx, float scale_log2,
+                       float* ws_acc, float* ws_ml, uint16_t* out, int64_t osb, int64_t osh,
+                       int32_t* err_count, hipStream_t s) {
   const int Wg = W / HG > 0 ? W / HG : 1;  // workgroups of HG waves
+  const int RPH = max_q_len * G;           // workspace rows per head
   // largest element offset: last slot's last head's row end
   const bool off32 = num_slots * kvs_slot + KVH * kvs_head + D < (int64_t(1) << 31);
   if (off32)
     decode_balanced_kernel<Tag, D, true, HG><<<dim3(static_cast<unsigned>(Wg)), 64 * HG, 0, s>>>(
-        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens, B,
-        KVH, G, max_ctx, scale_log2, Wg, ws_acc, ws_ml, out, osb, osh, err_count);
+        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens,
+        cu_q, B, KVH, G, RPH, max_ctx, scale_log2, Wg, ws_acc, ws_ml, out, osb, osh, err_count);
   else
     decode_balanced_kernel<Tag, D, false, HG><<<dim3(static_cast<unsigned>(Wg)), 64 * HG, 0, s>>>(
-        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens, B,
-        KVH, G, max_ctx, scale_log2, Wg, ws_acc, ws_ml, out, osb, osh, err_count);
+        q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head, bt, bt_stride, log2_bs, ctx_lens,
+        cu_q, B, KVH, G, RPH, max_ctx, scale_log2, Wg, ws_acc, ws_ml, out, osb, osh, err_count);
   const int st = dsp_launch_status();
   if (st != DSP_OK) return st;
   const int Hq = KVH * G;
-  decode_balanced_combine_kernel<Tag, D><<<dim3(Hq, B), 256, 0, s>>>(
-      ws_acc, ws_ml, ctx_lens, B, KVH, G, max_ctx, Wg, HG, out, osb, osh, err_count);
+  decode_balanced_combine_kernel<Tag, D><<<dim3(Hq, B, max_q_len), 256, 0, s>>>(
+      ws_acc, ws_ml, ctx_lens, cu_q, B, KVH, G, RPH, max_ctx, Wg, HG, out, osb, osh, err_count);
   return dsp_launch_status();
 }
 
@@ -527,26 +552,31 @@ template <typename Tag, int D>
 int launch_balanced_d(int W, const uint16_t* q, int64_t qsb, int64_t qsh, const uint16_t* kc,
                       const uint16_t* vc, int64_t num_slots, int64_t kvs_slot, int64_t kvs_head,
                       const int32_t* bt, int64_t bt_stride, int32_t log2_bs,
-                      const int32_t* ctx_lens, int32_t B, int32_t KVH, int32_t G, int32_t max_ctx,
-                      float scale_log2, float* ws_acc, float* ws_ml, uint16_t* out, int64_t osb,
-                      int64_t osh, int32_t* err_count, hipStream_t s) {
+                      const int32_t* ctx_lens, const int32_t* cu_q, int32_t max_q_len,
+                      int32_t B, int32_t KVH, int32_t G, int32_t max_ctx, float scale_log2,
+                      float* ws_acc, float* ws_ml, uint16_t* out, int64_t osb, int64_t osh,
+                      int32_t* err_count, hipStream_t s) {
   switch (dsp_detail::balanced_head_group(KVH)) {
     case 8:
       return launch_balanced_hg<Tag, D, 8>(W, q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head,
-                                           bt, bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx,
-                                           scale_log2, ws_acc, ws_ml, out, osb, osh, err_count, s);
+                                           bt, bt_stride, log2_bs, ctx_lens, cu_q, max_q_len, B,
+                                           KVH, G, max_ctx, scale_log2, ws_acc, ws_ml, out, osb,
+                                           osh, err_count, s);
     case 4:
       return launch_balanced_hg<Tag, D, 4>(W, q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head,
-                                           bt, bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx,
-                                           scale_log2, ws_acc, ws_ml, out, osb, osh, err_count, s);
+                                           bt, bt_stride, log2_bs, ctx_lens, cu_q, max_q_len, B,
+                                           KVH, G, max_ctx, scale_log2, ws_acc, ws_ml, out, osb,
+                                           osh, err_count, s);
     case 2:
       return launch_balanced_hg<Tag, D, 2>(W, q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head,
-                                           bt, bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx,
-                                           scale_log2, ws_acc, ws_ml, out, osb, osh, err_count, s);
+                                           bt, bt_stride, log2_bs, ctx_lens, cu_q, max_q_len, B,
+                                           KVH, G, max_ctx, scale_log2, ws_acc, ws_ml, out, osb,
+                                           osh, err_count, s);
     default:
       return launch_balanced_hg<Tag, D, 1>(W, q, qsb, qsh, kc, vc, num_slots, kvs_slot, kvs_head,
-                                           bt, bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx,
-                                           scale_log2, ws_acc, ws_ml, out, osb, osh, err_count, s);
+                                           bt, bt_stride, log2_bs, ctx_lens, cu_q, max_q_len, B,
+                                           KVH, G, max_ctx, scale_log2, ws_acc, ws_ml, out, osb,
+                                           osh, err_count, s);
   }
 }
 
@@ -597,30 +627,33 @@ int32_t balanced_workers(int32_t B, int32_t KVH, int32_t max_ctx) {
   return static_cast<int32_t>(want < cap ? want : cap);
 }
 
-size_t balanced_workspace_bytes(int32_t B, int32_t KVH, int32_t G, int32_t D, int32_t max_ctx) {
+size_t balanced_workspace_bytes(int32_t B, int32_t KVH, int32_t rows_per_head, int32_t D,
+                                int32_t max_ctx) {
   const int64_t slots = int64_t(B) * KVH + balanced_workers(B, KVH, max_ctx);
-  return size_t(slots) * G * (size_t(D) + 2) * sizeof(float);
+  return size_t(slots) * rows_per_head * (size_t(D) + 2) * sizeof(float);
 }
 
 int balanced_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
                     const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,
                     int64_t kv_stride_slot, int64_t kv_stride_head, const int32_t* block_table,
-                    int64_t bt_stride, int32_t log2_bs, const int32_t* ctx_lens, int32_t B,
-                    int32_t KVH, int32_t G, int32_t D, float scale_log2, int32_t max_ctx,
-                    float* workspace, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
-                    bool f16, int32_t* err_count, hipStream_t s) {
+                    int64_t bt_stride, int32_t log2_bs, const int32_t* ctx_lens,
+                    const int32_t* cu_q, int32_t max_q_len, int32_t B, int32_t KVH, int32_t G,
+                    int32_t D, float scale_log2, int32_t max_ctx, float* workspace,
+                    uint16_t* out, int64_t o_stride_b, int64_t o_stride_h, bool f16,
+                    int32_t* err_count, hipStream_t s) {
   const int32_t W = balanced_workers(B, KVH, max_ctx);
   float* ws_acc = workspace;
-  float* ws_ml = ws_acc + (int64_t(B) * KVH + W) * G * D;
+  float* ws_ml = ws_acc + (int64_t(B) * KVH + W) * max_q_len * G * D;
   if (!f16)
     return launch_balanced<Bf16Tag>(D, W, q, q_stride_b, q_stride_h, k_cache, v_cache,
                                     num_slots, kv_stride_slot, kv_stride_head, block_table,
-                                    bt_stride, log2_bs, ctx_lens, B, KVH, G, max_ctx, scale_log2,
-                                    ws_acc, ws_ml, out, o_stride_b, o_stride_h, err_count, s);
+                                    bt_stride, log2_bs, ctx_lens, cu_q, max_q_len, B, KVH, G,
+                                    max_ctx, scale_log2, ws_acc, ws_ml, out, o_stride_b,
+                                    o_stride_h, err_count, s);
   return launch_balanced<F16Tag>(D, W, q, q_stride_b, q_stride_h, k_cache, v_cache, num_slots,
                                  kv_stride_slot, kv_stride_head, block_table, bt_stride, log2_bs,
-                                 ctx_lens, B, KVH, G, max_ctx, scale_log2, ws_acc, ws_ml, out,
-                                 o_stride_b, o_stride_h, err_count, s);
+                                 ctx_lens, cu_q, max_q_len, B, KVH, G, max_ctx, scale_log2,
+                                 ws_acc, ws_ml, out, o_stride_b, o_stride_h, err_count, s);
 }
 
 }  // namespace dsp_detail

@@ -20,21 +20,26 @@ int mq_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, const u
               float* ws_acc, float* ws_ml, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
               bool f16, int32_t* err_count, hipStream_t s);
 
-// Balanced split-K decode on block tables (decode_balanced.hip): every wave of the launch
-// takes an equal share of the (sequence, KV head, 16-key unit) work.  `applies` says
-// whether the shape is one it serves; the workspace is balanced_workspace_bytes() long.
+// Balanced split-K attention on block tables (decode_balanced.hip): every wave of the
+// launch takes an equal share of the (sequence, KV head, 16-key unit) work.  Decode:
+// cu_q null, max_q_len 1, q/out rows indexed by sequence.  Multi-query (verify): cu_q as
+// for dsp_paged_mq_attention, max_q_len * G <= 16 query rows per KV head, q/out rows
+// indexed by token.  `applies` says whether the shape is one it serves; the workspace is
+// balanced_workspace_bytes(..., max_q_len * G, ...) long.
 bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
                              int32_t block_size);
 int32_t balanced_workers(int32_t B, int32_t KVH, int32_t max_ctx);
 int balanced_head_group(int32_t KVH);
-size_t balanced_workspace_bytes(int32_t B, int32_t KVH, int32_t G, int32_t D, int32_t max_ctx);
+size_t balanced_workspace_bytes(int32_t B, int32_t KVH, int32_t rows_per_head, int32_t D,
+                                int32_t max_ctx);
 int balanced_decode(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
                     const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,
                     int64_t kv_stride_slot, int64_t kv_stride_head, const int32_t* block_table,
-                    int64_t bt_stride, int32_t log2_bs, const int32_t* ctx_lens, int32_t B,
-                    int32_t KVH, int32_t G, int32_t D, float scale_log2, int32_t max_ctx,
-                    float* workspace, uint16_t* out, int64_t o_stride_b, int64_t o_stride_h,
-                    bool f16, int32_t* err_count, hipStream_t s);
+                    int64_t bt_stride, int32_t log2_bs, const int32_t* ctx_lens,
+                    const int32_t* cu_q, int32_t max_q_len, int32_t B, int32_t KVH, int32_t G,
+                    int32_t D, float scale_log2, int32_t max_ctx, float* workspace,
+                    uint16_t* out, int64_t o_stride_b, int64_t o_stride_h, bool f16,
+                    int32_t* err_count, hipStream_t s);
 
 // Long query blocks (chunked prefill) on the 128-row FlashAttention-style tile
 // (paged_prefill.hip): the semantics, arguments and workspace layout of

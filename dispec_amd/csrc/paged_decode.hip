@@ -527,8 +527,9 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
     DSP_HOST_CHECK(dsp_aligned(workspace, 16), DSP_EALIGN);
     return dsp_detail::balanced_decode(qh, q_stride_b, q_stride_h, kh, vh, num_slots,
                                        kv_stride_slot, kv_stride_head, table, table_stride,
-                                       log2_bs, ctx_lens, B, KVH, G, D, scale_log2, max_ctx,
-                                       static_cast<float*>(workspace), oh, o_stride_b,
+                                       log2_bs, ctx_lens, nullptr, 1, B, KVH, G, D,
+                                       scale_log2, max_ctx, static_cast<float*>(workspace), oh,
+                                       o_stride_b,
                                        o_stride_h, dtype == DSP_F16, err_count, s);
   }
   int P = partition_tokens > 0 ? partition_tokens

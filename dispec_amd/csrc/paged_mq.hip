@@ -454,16 +454,41 @@ extern "C" int dsp_paged_mq_partition_tokens(int32_t B, int32_t Hq, int32_t KVH,
   return static_cast<int32_t>(best_p);
 }
 
-extern "C" size_t dsp_paged_mq_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
-                                               int32_t max_q_len, int32_t max_ctx,
-                                               int32_t partition_tokens) {
-  if (B <= 0 || KVH <= 0 || Hq % KVH != 0 || max_q_len <= 0 || max_ctx <= 0 ||
-      partition_tokens <= 0)
-    return 0;
-  const int64_t np = (int64_t(max_ctx) + partition_tokens - 1) / partition_tokens;
+namespace {
+
+// Short query blocks on the balanced split-K kernel: automatic partition, no shared prefix,
+// every query row of a KV head in one MFMA tile, and a shape that kernel serves.
+bool balanced_verify_applies(int32_t B, int32_t Hq, int32_t KVH, int32_t D, int32_t max_q_len,
+                             int32_t max_ctx, int32_t block_size) {
+  return KVH > 0 && Hq % KVH == 0 && max_q_len > 0 && int64_t(max_q_len) * (Hq / KVH) <= 16 &&
+         dsp_detail::balanced_decode_applies(B, KVH, D, max_ctx, block_size);
+}
+
+size_t fixed_mq_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
+                                int32_t max_q_len, int32_t max_ctx, int32_t P) {
+  const int64_t np = (int64_t(max_ctx) + P - 1) / P;
   if (np <= 1) return 0;
   return size_t(B) * KVH * mq_tiles(max_q_len, Hq / KVH) * np * 16 * (size_t(D) + 2) *
          sizeof(float);
+}
+
+}  // namespace
+
+extern "C" size_t dsp_paged_mq_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
+                                               int32_t max_q_len, int32_t max_ctx,
+                                               int32_t partition_tokens) {
+  if (B <= 0 || KVH <= 0 || Hq % KVH != 0 || max_q_len <= 0 || max_ctx <= 0) return 0;
+  if (partition_tokens == DSP_SPLIT_BALANCED)
+    return balanced_verify_applies(B, Hq, KVH, D, max_q_len, max_ctx, 16)
+               ? dsp_detail::balanced_workspace_bytes(B, KVH, max_q_len * (Hq / KVH), D,
+                                                      max_ctx)
+               : 0;
+  if (partition_tokens < 0) return 0;
+  // 0: the partition the launch picks from the shape
+  return fixed_mq_workspace_bytes(
+      B, Hq, KVH, D, max_q_len, max_ctx,
+      partition_tokens > 0 ? partition_tokens
+                           : dsp_paged_mq_partition_tokens(B, Hq, KVH, D, max_q_len, max_ctx));
 }
 
 namespace {
@@ -495,6 +520,27 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                      dsp_aligned(v_cache, 16),
                  DSP_EALIGN);
   const int G = Hq / KVH;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool f16 = dtype == DSP_F16;
+  if (partition_tokens == DSP_SPLIT_BALANCED) {
+    // short query blocks on the balanced split: every wave takes an equal share of the keys
+    DSP_HOST_CHECK(prefix_tokens == 0, DSP_EINVAL);
+    DSP_HOST_CHECK(num_slots > 0 && num_slots < (int64_t(1) << 31) &&
+                       balanced_verify_applies(B, Hq, KVH, D, max_q_len, max_ctx, block_size),
+                   DSP_EUNSUPPORTED);
+    const size_t need = dsp_detail::balanced_workspace_bytes(B, KVH, max_q_len * G, D, max_ctx);
+    DSP_HOST_CHECK(workspace_bytes >= need && workspace != nullptr, DSP_EWORKSPACE);
+    DSP_HOST_CHECK(dsp_aligned(workspace, 16), DSP_EALIGN);
+    return dsp_detail::balanced_decode(
+        static_cast<const uint16_t*>(q), q_stride_t, q_stride_h,
+        static_cast<const uint16_t*>(k_cache), static_cast<const uint16_t*>(v_cache),
+        num_slots, kv_stride_slot, kv_stride_head, block_table, bt_stride,
+        dsp_log2i(block_size), ctx_lens, cu_q, max_q_len, B, KVH, G, D, scale_log2, max_ctx,
+        static_cast<float*>(workspace), static_cast<uint16_t*>(out), o_stride_t, o_stride_h,
+        f16, err_count, s);
+  }
+  DSP_HOST_CHECK(partition_tokens >= 0, DSP_EINVAL);
   const int64_t tiles = mq_tiles(max_q_len, G);
   int P = partition_tokens;
   if (P <= 0)
@@ -511,20 +557,17 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
   const int first_part = prefix_tokens / P;
   DSP_HOST_CHECK(num_parts <= kMaxParts, DSP_EINVAL);
   DSP_HOST_CHECK(tiles * num_parts < (int64_t(1) << 31), DSP_EINVAL);
-  const size_t need = dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, max_q_len, max_ctx, P);
+  const size_t need = fixed_mq_workspace_bytes(B, Hq, KVH, D, max_q_len, max_ctx, P);
   DSP_HOST_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr), DSP_EWORKSPACE);
   DSP_HOST_CHECK(need == 0 || dsp_aligned(workspace, 16), DSP_EALIGN);
   float* ws_acc = static_cast<float*>(workspace);
   float* ws_ml = need ? ws_acc + int64_t(B) * KVH * tiles * num_parts * 16 * D : nullptr;
-  const float scale_log2 = scale * 1.4426950408889634f;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* qh = static_cast<const uint16_t*>(q);
   const uint16_t* kh = static_cast<const uint16_t*>(k_cache);
   const uint16_t* vh = static_cast<const uint16_t*>(v_cache);
   uint16_t* oh = static_cast<uint16_t*>(out);
   const int32_t lbs = dsp_log2i(block_size);
   const int32_t tm = static_cast<int32_t>(tiles);
-  const bool f16 = dtype == DSP_F16;
   int st = DSP_OK;
   int ws_parts = num_parts, fixed_parts = 0;
   if (prefix_tokens > 0) {

@@ -117,17 +117,16 @@ def decode_workspace(batch, num_heads, num_kv_heads, head_dim, max_ctx, device):
 
 
 def mq_workspace(batch, num_heads, num_kv_heads, head_dim, max_q_len, max_ctx, device,
-                 shared_prefix_tokens=0):
+                 shared_prefix_tokens=0, balanced=False):
     """A float32 split-K workspace for every `paged_mq_attention` launch of this shape with
-    the automatic partition, or None when it needs none.  One buffer serves all layers of a
-    forward: the launches run in stream order."""
+    the automatic partition (or the balanced split), or None when it needs none.  One
+    buffer serves all layers of a forward: the launches run in stream order."""
     L = _lib.lib()
     if shared_prefix_tokens:
         P = L.dsp_paged_mq_shared_prefix_partition_tokens(
             batch, num_heads, num_kv_heads, head_dim, max_q_len, max_ctx, shared_prefix_tokens)
     else:
-        P = L.dsp_paged_mq_partition_tokens(batch, num_heads, num_kv_heads, head_dim,
-                                            max_q_len, max_ctx)
+        P = _lib.DSP_SPLIT_BALANCED if balanced else 0
     need = L.dsp_paged_mq_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, max_q_len,
                                           max_ctx, P)
     return torch.empty(need // 4 + 1, dtype=torch.float32, device=device) if need else None
@@ -135,7 +134,8 @@ def mq_workspace(batch, num_heads, num_kv_heads, head_dim, max_q_len, max_ctx, d
 
 def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_groups,
                        block_size=16, scale=None, max_q_len=None, max_ctx=None, out=None,
-                       err=None, partition_tokens=0, workspace=None, shared_prefix_tokens=0):
+                       err=None, partition_tokens=0, workspace=None, shared_prefix_tokens=0,
+                       balanced=False):
     """Multi-query paged attention: speculative verify, chunked and fresh prefill.
 
     Per sequence b, rows q[cu_q[b]:cu_q[b+1]] are the last q_len_b tokens of a ctx_b-token
@@ -149,6 +149,10 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
                  which costs a device->host copy)
     partition_tokens: split-K key partition (0: chosen from the shape); workspace: an
                  optional preallocated fp32 buffer for the partial results
+    balanced:    short query blocks (max_q_len * kv_groups <= 16) on the balanced split-K
+                 kernel instead of key partitions: every wave takes an equal share of the
+                 keys, which pays when one context is much longer than the others
+                 (DSP_SPLIT_BALANCED)
     shared_prefix_tokens: > 0 when the first that many context tokens of every sequence
                  are the same physical blocks (copy-on-write forks, prefix-cache hits) and
                  every query sees them all: they are attended once for the whole batch
@@ -186,12 +190,15 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
         raise ValueError("out must have q's shape and dtype with head_dim contiguous")
     L = _lib.lib()
     sp = int(shared_prefix_tokens)
+    if balanced and (sp or partition_tokens):
+        raise ValueError("balanced excludes shared_prefix_tokens and partition_tokens")
     if sp:
         P = partition_tokens or L.dsp_paged_mq_shared_prefix_partition_tokens(
             B, Hq, KVH, D, int(max_q_len), int(max_ctx), sp)
+    elif balanced:
+        P = _lib.DSP_SPLIT_BALANCED
     else:
-        P = partition_tokens or L.dsp_paged_mq_partition_tokens(B, Hq, KVH, D, int(max_q_len),
-                                                                int(max_ctx))
+        P = int(partition_tokens)   # 0: the library picks the partition
     need = L.dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, int(max_q_len), int(max_ctx), P)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)

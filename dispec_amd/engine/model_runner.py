@@ -31,9 +31,9 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from dispec_amd import _lib
 from dispec_amd.engine.hip_attn import (decode_workspace, mq_workspace,
-                                       paged_decode_attention_blocks,
-                                        paged_mq_attention)
+                                       paged_decode_attention_blocks, paged_mq_attention)
 from dispec_amd.engine.hip_prologue import qk_norm_rope_append
 from dispec_amd.kv.paged_cache import PagedKVCache
 
@@ -59,6 +59,7 @@ class _Batch:
     decode: bool
     workspace: torch.Tensor | None = None
     shared_prefix: int = 0   # leading context tokens all sequences share (0: none used)
+    balanced: bool = False   # short query blocks on the balanced split-K kernel
 
 
 class ModelRunner:
@@ -93,6 +94,11 @@ class ModelRunner:
         # this many leading tokens (fewer gain nothing over per-sequence attention)
         self.shared_prefix_min_seqs = 4
         self.shared_prefix_min_tokens = 512
+        # balanced split for verify batches whose keys per resident workgroup fall below
+        # this fraction of the fixed split's partition (see _prefer_balanced)
+        self.balanced_key_fraction = 0.6
+        self._cus = (torch.cuda.get_device_properties(self.device).multi_processor_count
+                     if self.device.type == "cuda" else 256)
 
     def _build_fused(self) -> bool:
         """One GEMM for q/k/v and one for gate/up per layer (model_runner.py:93-118)."""
@@ -138,9 +144,32 @@ class ModelRunner:
         decode = all(m.q_len == 1 for m in seq_meta)
         shared = self._shared_prefix(seq_meta, host[2 * B + 1:].view(B, width),
                                      cache.block_size)
+        max_q_len = max(m.q_len for m in seq_meta)
+        max_ctx = width * cache.block_size
+        balanced = (not decode and not shared and
+                    self._prefer_balanced(seq_meta, max_q_len, max_ctx, cache.block_size))
         return _Batch(block_table=dev[2 * B + 1:].view(B, width), ctx_lens=dev[:B],
-                      cu_q=dev[B:2 * B + 1], max_q_len=max(m.q_len for m in seq_meta),
-                      max_ctx=width * cache.block_size, decode=decode, shared_prefix=shared)
+                      cu_q=dev[B:2 * B + 1], max_q_len=max_q_len, max_ctx=max_ctx,
+                      decode=decode, shared_prefix=shared, balanced=balanced)
+
+    def _prefer_balanced(self, seq_meta: list[SeqMeta], max_q_len: int, max_ctx: int,
+                         bs: int) -> bool:
+        """Whether a batch of short query blocks (verify) runs on the balanced split-K
+        kernel rather than fixed key partitions.  Fixed partitions are sized from max_ctx
+        for every sequence; when the batch's keys per resident 16-row workgroup (three per
+        CU) fall below `balanced_key_fraction` of that partition, the longest sequence's
+        partitions run as a tail on a mostly idle GPU, and the balanced split, which gives
+        every wave the same share of the keys, wins (one 32k context among 15 of 512, Qwen3
+        heads, 5 queries: 50 against 92 us; similar lengths: fixed partitions 4-6 %
+        faster)."""
+        B = len(seq_meta)
+        if (max_q_len * self.kv_groups > 16 or B > 512 or bs < 16
+                or self.head_dim not in (32, 64, 128)):
+            return False
+        P = _lib.lib().dsp_paged_mq_partition_tokens(B, self.num_heads, self.num_kv_heads,
+                                                     self.head_dim, max_q_len, max_ctx)
+        keys = sum(m.ctx_len for m in seq_meta) * self.num_kv_heads
+        return keys < self.balanced_key_fraction * P * 3 * self._cus
 
     def _shared_prefix(self, seq_meta: list[SeqMeta], table: torch.Tensor, bs: int) -> int:
         """Leading context tokens whose blocks every sequence's table shares and every query
@@ -186,7 +215,7 @@ class ModelRunner:
                 q, cache.key[layer_idx], cache.value[layer_idx], batch.block_table, batch.cu_q,
                 batch.ctx_lens, self.kv_groups, block_size=cache.block_size, scale=self.scale,
                 max_q_len=batch.max_q_len, max_ctx=batch.max_ctx, workspace=batch.workspace,
-                shared_prefix_tokens=batch.shared_prefix)
+                shared_prefix_tokens=batch.shared_prefix, balanced=batch.balanced)
         return attn.o_proj(o.reshape(T, self.num_heads * self.head_dim))
 
     @torch.inference_mode()
@@ -216,7 +245,8 @@ class ModelRunner:
             else:
                 batch.workspace = mq_workspace(B, self.num_heads, self.num_kv_heads,
                                                self.head_dim, batch.max_q_len, batch.max_ctx,
-                                               cache.key.device, batch.shared_prefix)
+                                               cache.key.device, batch.shared_prefix,
+                                               batch.balanced)
         for i, layer in enumerate(self.layers):
             h = layer.input_layernorm(x)
             x = x + self._attention(layer, h, cos, sin, write_slots, cache, i, batch)

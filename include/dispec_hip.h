@@ -45,6 +45,10 @@ enum dsp_status {
   DSP_EWORKSPACE = -4     /* workspace smaller than dsp_*_workspace_bytes() */
 };
 
+/* partition_tokens value of dsp_paged_mq_attention (and its workspace size) that asks for
+ * the balanced split-K kernel instead of fixed key partitions. */
+enum dsp_split { DSP_SPLIT_BALANCED = -1 };
+
 /* Human-readable text for a status code (static storage; never NULL). */
 const char* dsp_error_string(int status);
 
@@ -185,6 +189,14 @@ int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  *   partition_tokens : split-K key partition (multiple of 128, at most 64 partitions of
  *                max_ctx); 0 picks one from the shape.  More than one partition needs
  *                `workspace` (dsp_paged_mq_workspace_bytes) and a merge kernel.
+ *                DSP_SPLIT_BALANCED: the balanced split-K kernel of dsp_paged_decode --
+ *                every wave of the launch takes an equal share of the (sequence, KV head,
+ *                16-key unit) work, so one long context among short ones does not leave a
+ *                tail of its partitions on an idle GPU (1 x 32k + 15 x 512 contexts, Qwen3
+ *                heads, 5 queries: 50 against 92 us); contexts of similar length run 4-6 %
+ *                faster on fixed partitions.  Needs max_q_len * G <= 16, blocks of >= 16
+ *                tokens, B <= 512, D in {32, 64, 128} (else DSP_EUNSUPPORTED) and always
+ *                `workspace` (dsp_paged_mq_workspace_bytes with DSP_SPLIT_BALANCED).
  * dtype DSP_BF16 / DSP_F16; D in {32, 64, 128}; any G = Hq / KVH.  A sequence with
  * q_len > ctx or ctx > max_ctx is counted in err_count and its rows written as zeros.
  * Batches with max_q_len * G >= 128 (D 64 or 128, blocks of >= 16 tokens) run on a

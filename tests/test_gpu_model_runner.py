@@ -166,6 +166,28 @@ def test_decode_of_forked_sequences_uses_the_shared_prefix():
         cur += 1
 
 
+@pytest.mark.parametrize("family", sorted(MODELS))
+def test_verify_of_skewed_sequences_uses_the_balanced_split(family):
+    """A 5-token verify over sequences of 600, 20, 45 and 9 tokens (independent prompts,
+    no shared blocks): the runner picks the balanced split-K kernel (its keys per resident
+    workgroup are far below the fixed split's partition) and the logits match the native
+    path sequence by sequence."""
+    from dispec_amd.engine.model_runner import SeqMeta
+    gm, cm = _pair(family)
+    both = _Both(gm, cm, num_blocks=96)
+    g = torch.Generator().manual_seed(14)
+    lens = [600, 20, 45, 9]
+    for sid, n in enumerate(lens):
+        both.forward([(sid, torch.randint(0, 128, (n,), generator=g).tolist(), 0)])
+    drafts = [torch.randint(0, 128, (5,), generator=g).tolist() for _ in lens]
+    got, ref = both.forward([(sid, drafts[sid], n) for sid, n in enumerate(lens)])
+    assert _cos(got, ref).min() >= 0.999
+    mgr = both.cache.manager
+    meta = [SeqMeta(list(mgr.block_table(s).block_ids), 5, n + 5) for s, n in enumerate(lens)]
+    batch = both.runner._batch(meta, both.cache)
+    assert batch.balanced and not batch.shared_prefix and not batch.decode
+
+
 def test_rejects_other_backends():
     from dispec_amd.engine.model_runner import ModelRunner
     with pytest.raises(ValueError, match="hip"):
