@@ -7,7 +7,7 @@
 // Work split.  The decode work of one launch is the list of (sequence b, group of HG KV
 // heads, 16-key unit) triples in sequence-major, then head-group, then key order; a
 // (sequence, head group) pair is a "segment".  With C units in all and W workers -- one
-// workgroup of HG waves each, at most as many as the GPU holds at once -- worker w takes
+// workgroup of HG waves each, at most one wave per SIMD of the GPU -- worker w takes
 // units [w*C/W, (w+1)*C/W), wave i of it KV head HG*group + i of every unit.  Every wave
 // therefore reads the same number of K/V bytes (to one unit) whatever the spread of context
 // lengths, and all of them finish together: there is no tail of long partitions running on
@@ -620,7 +620,12 @@ bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
 }
 
 int32_t balanced_workers(int32_t B, int32_t KVH, int32_t max_ctx) {
-  const int64_t cap = int64_t(dsp_detail::device_cus()) * 4 * kOcc;
+  // One worker wave per SIMD: every CU gets the same number of workgroups (4 / HG of
+  // them), and fewer, longer key streams over the randomly placed blocks read faster than
+  // three waves per SIMD (config 3 387 -> 377-379 us, one 32k context among 15 short
+  // 50.5 -> 46-47, config 2 -1 %); 1.5 or 0.75 waves per SIMD load the CUs unevenly
+  // (config 3 410-414 us).
+  const int64_t cap = int64_t(dsp_detail::device_cus()) * 4;
   const int64_t cmax = int64_t(B) * KVH * ((int64_t(max_ctx) + 15) >> kLog2Unit);
   int64_t want = (cmax + kMinUnits - 1) / kMinUnits;
   if (want < 1) want = 1;

@@ -160,7 +160,7 @@ class ModelRunner:
         CU) fall below `balanced_key_fraction` of that partition, the longest sequence's
         partitions run as a tail on a mostly idle GPU, and the balanced split, which gives
         every wave the same share of the keys, wins (one 32k context among 15 of 512, Qwen3
-        heads, 5 queries: 50 against 92 us; similar lengths: fixed partitions 4-6 %
+        heads, 5 queries: 44 against 93 us; similar lengths: fixed partitions 0-5 %
         faster)."""
         B = len(seq_meta)
         if (max_q_len * self.kv_groups > 16 or B > 512 or bs < 16

@@ -193,7 +193,7 @@ int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  *                every wave of the launch takes an equal share of the (sequence, KV head,
  *                16-key unit) work, so one long context among short ones does not leave a
  *                tail of its partitions on an idle GPU (1 x 32k + 15 x 512 contexts, Qwen3
- *                heads, 5 queries: 50 against 92 us); contexts of similar length run 4-6 %
+ *                heads, 5 queries: 44 against 93 us); contexts of similar length run 0-5 %
  *                faster on fixed partitions.  Needs max_q_len * G <= 16, blocks of >= 16
  *                tokens, B <= 512, D in {32, 64, 128} (else DSP_EUNSUPPORTED) and always
  *                `workspace` (dsp_paged_mq_workspace_bytes with DSP_SPLIT_BALANCED).

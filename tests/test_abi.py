@@ -96,10 +96,12 @@ def test_partition_and_workspace_sizing(lib):
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, 512) == 0   # one partition
     # automatic split: room for the balanced split (B*KVH + waves slots of G rows) and for
     # the fixed partitions a slot-table launch of the same shape picks.  Without a GPU the
-    # library assumes 256 CUs: 256 * 4 SIMDs * 3 waves = 3072 waves.
+    # library assumes 256 CUs: one worker wave per SIMD, 256 * 4 = 1024 waves.
     fixed = 16 * 32 * 32 * 130 * 4                  # 1024-token partitions
-    balanced = (16 * 8 + 3072) * 4 * 130 * 4
+    balanced = (16 * 8 + 1024) * 4 * 130 * 4
     assert lib.dsp_paged_decode_workspace_bytes(16, 32, 8, 128, 32768, 0) == max(fixed, balanced)
+    assert lib.dsp_paged_decode_workspace_bytes(512, 32, 8, 128, 4096, 0) >= \
+        (512 * 8 + 1024) * 4 * 130 * 4
     # a small launch: at least 4 units of 16 keys per wave -> 4*2*ceil(500/16)/4 = 64 waves
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, 0) == (4 * 2 + 64) * 7 * 66 * 4
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 3, 64, 500, 0) == 0     # 14 % 3 != 0

@@ -156,5 +156,5 @@ def test_workspace_covers_the_balanced_split():
     B, Hq, KVH, D, ql, ctx = 32, 16, 8, 128, 5, 4096
     need = L.dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, ql, ctx, _lib.DSP_SPLIT_BALANCED)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    workers = min(B * KVH * ctx // 16 // 4, cus * 4 * 3)
+    workers = min(B * KVH * ctx // 16 // 4, cus * 4)
     assert need >= (B * KVH + workers) * ql * (Hq // KVH) * (D + 2) * 4
