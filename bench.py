@@ -155,7 +155,8 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
                                             cache.key.shape[1], bt.data_ptr(), bt.stride(0), bs,
                                             B, KVH, ctx, waves, sink.data_ptr(), stream), "probe")
     stream_s = _time_gpu(torch, stream_probe, 10)
-    # best of 1024, 2048 and 4096 waves
+    # best of 256, 512 and 1024 workgroups of 4 waves (one, two and four per CU): the
+    # decode's access pattern, 4 heads of each slot row read side by side
     slice_s = min(_time_gpu(torch, lambda: slice_probe(w), 10) for w in (8, 16, 32))
     read_ceiling = span.numel() * 2 / stream_s / 1e9
     pattern_ceiling = B * ctx * KVH * D * 2 * 2 / slice_s / 1e9

@@ -31,22 +31,25 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const dsp_u32x4* __res
   if (r == 0x9e3779b9u) sink[0] = r;
 }
 
-// One wave per (sequence, KV head, share of its keys): per 32 keys it reads the head's
-// row of K and of V for every key (16 bytes per lane, 4 rows per load), addressed through
-// the block table exactly as the decode kernels address the pool.
-__global__ __launch_bounds__(64) void slice_read_kernel(const uint16_t* __restrict__ kc,
-                                                        const uint16_t* __restrict__ vc,
-                                                        int64_t num_slots,
-                                                        const int32_t* __restrict__ bt,
-                                                        int64_t bt_stride, int32_t log2_bs,
-                                                        int32_t KVH, int32_t keys_per_wave,
-                                                        int32_t waves_per_seg,
-                                                        uint32_t* __restrict__ sink) {
+// One workgroup of HG waves per (sequence, group of HG KV heads, share of its keys), wave
+// i reading head HG*group + i, as the balanced decode kernel groups its waves: per 32 keys
+// a wave reads its head's row of K and of V for every key (16 bytes per lane, 4 rows per
+// load), addressed through the block table exactly as the decode kernels address the pool.
+template <int HG>
+__global__ __launch_bounds__(64 * HG) void slice_read_kernel(const uint16_t* __restrict__ kc,
+                                                             const uint16_t* __restrict__ vc,
+                                                             int64_t num_slots,
+                                                             const int32_t* __restrict__ bt,
+                                                             int64_t bt_stride, int32_t log2_bs,
+                                                             int32_t KVH, int32_t keys_per_wave,
+                                                             int32_t waves_per_seg,
+                                                             uint32_t* __restrict__ sink) {
   constexpr int D = 128;
   const int w = blockIdx.x;
+  const int NG = KVH / HG;
   const int seg = w / waves_per_seg, part = w % waves_per_seg;
-  const int b = seg / KVH, h = seg % KVH;
-  const int lane = threadIdx.x;
+  const int b = seg / NG, h = (seg % NG) * HG + int(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
   const int bmask = (1 << log2_bs) - 1;
   dsp_u32x4 acc = {0u, 0u, 0u, 0u};
   const int k0 = part * keys_per_wave;
@@ -129,11 +132,19 @@ extern "C" int dsp_probe_slice_read(const void* k_cache, const void* v_cache, in
   DSP_HOST_CHECK(bt_stride * block_size >= ctx, DSP_EINVAL);
   DSP_HOST_CHECK(dsp_aligned(k_cache, 16) && dsp_aligned(v_cache, 16), DSP_EALIGN);
   DSP_HOST_CHECK(num_slots > 0, DSP_EINVAL);
-  const int64_t grid = int64_t(B) * KVH * waves_per_seq_head;
+  const int HG = KVH % 4 == 0 ? 4 : 1;  // heads read side by side, as the decode kernel does
+  const int64_t grid = int64_t(B) * (KVH / HG) * waves_per_seq_head;
   DSP_HOST_CHECK(grid < (int64_t(1) << 31), DSP_EINVAL);
-  slice_read_kernel<<<dim3(static_cast<unsigned>(grid)), 64, 0, static_cast<hipStream_t>(stream)>>>(
-      static_cast<const uint16_t*>(k_cache), static_cast<const uint16_t*>(v_cache), num_slots,
-      block_table,
-      bt_stride, dsp_log2i(block_size), KVH, ctx / waves_per_seq_head, waves_per_seq_head, sink);
+  const auto* kh = static_cast<const uint16_t*>(k_cache);
+  const auto* vh = static_cast<const uint16_t*>(v_cache);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (HG == 4)
+    slice_read_kernel<4><<<dim3(static_cast<unsigned>(grid)), 256, 0, st>>>(
+        kh, vh, num_slots, block_table, bt_stride, dsp_log2i(block_size), KVH,
+        ctx / waves_per_seq_head, waves_per_seq_head, sink);
+  else
+    slice_read_kernel<1><<<dim3(static_cast<unsigned>(grid)), 64, 0, st>>>(
+        kh, vh, num_slots, block_table, bt_stride, dsp_log2i(block_size), KVH,
+        ctx / waves_per_seq_head, waves_per_seq_head, sink);
   return dsp_launch_status();
 }

@@ -318,8 +318,10 @@ int dsp_qk_norm_rope_append(const void* q, int64_t q_stride_t, int64_t q_stride_
  *     aligned) once.
  *   dsp_probe_slice_read: the paged decode's access pattern without its arithmetic --
  *     for each (sequence, KV head) `waves_per_seq_head` waves read that head's 128-dim
- *     bf16 row of K and V for all `ctx` keys through `block_table`; caches are
- *     [num_slots, KVH, 128] contiguous; ctx a multiple of 32 * waves_per_seq_head.
+ *     bf16 row of K and V for all `ctx` keys through `block_table`, the waves of 4 heads
+ *     of the same keys side by side in one workgroup when KVH % 4 == 0 (as the balanced
+ *     decode kernel groups them); caches are [num_slots, KVH, 128] contiguous; ctx a
+ *     multiple of 32 * waves_per_seq_head.
  * Both store one word to `sink` only if what they read hashes to a sentinel. */
 int dsp_probe_stream_read(const void* buf, int64_t bytes, int32_t workgroups, uint32_t* sink,
                           dsp_stream_t stream);
