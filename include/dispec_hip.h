@@ -188,7 +188,8 @@ int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  *   max_q_len  : upper bound of q_len_b (sizes the grid).
  *   partition_tokens : split-K key partition (multiple of 128, at most 64 partitions of
  *                max_ctx); 0 picks one from the shape.  More than one partition needs
- *                `workspace` (dsp_paged_mq_workspace_bytes) and a merge kernel.
+ *                `workspace` (dsp_paged_mq_workspace_bytes with the same partition_tokens,
+ *                0 included) and a merge kernel.
  *                DSP_SPLIT_BALANCED: the balanced split-K kernel of dsp_paged_decode --
  *                every wave of the launch takes an equal share of the (sequence, KV head,
  *                16-key unit) work, so one long context among short ones does not leave a

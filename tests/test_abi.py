@@ -92,6 +92,16 @@ def test_partition_and_workspace_sizing(lib):
     assert lib.dsp_paged_mq_partition_tokens(32, 16, 8, 128, 5, 2688) == 896
     assert lib.dsp_paged_mq_partition_tokens(64, 16, 8, 128, 5, 704) == 768
     assert lib.dsp_paged_mq_partition_tokens(8, 16, 8, 128, 5, 2560) == 384
+    # multi-query workspace: 0 sizes the partition the launch picks; DSP_SPLIT_BALANCED the
+    # balanced split's pieces, (B*KVH + worker waves) slots of max_q_len * G rows
+    from dispec_amd import _lib
+    P = lib.dsp_paged_mq_partition_tokens(32, 16, 8, 128, 5, 2688)
+    assert lib.dsp_paged_mq_workspace_bytes(32, 16, 8, 128, 5, 2688, 0) == \
+        lib.dsp_paged_mq_workspace_bytes(32, 16, 8, 128, 5, 2688, P) == 32 * 8 * 3 * 16 * 130 * 4
+    assert lib.dsp_paged_mq_workspace_bytes(32, 16, 8, 128, 5, 2688, _lib.DSP_SPLIT_BALANCED) == \
+        (32 * 8 + 1024) * 10 * 130 * 4
+    # more than 16 query rows per KV head: no balanced split, no workspace for it
+    assert lib.dsp_paged_mq_workspace_bytes(32, 16, 8, 128, 9, 2688, _lib.DSP_SPLIT_BALANCED) == 0
     assert lib.dsp_paged_decode_workspace_bytes(16, 32, 8, 128, 32768, 512) == 16 * 32 * 64 * 130 * 4
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, 512) == 0   # one partition
     # automatic split: room for the balanced split (B*KVH + waves slots of G rows) and for
