@@ -77,24 +77,30 @@ __device__ __forceinline__ int wave_sum(int v) {
 }
 
 // Work units of sequence b.  Decode (cu_q null): its clamped context.  Multi-query: none
-// for an empty query block or a context outside [q_len, max_ctx] (the merge kernel writes
-// such a sequence's rows as zeros and counts it), else its context.
+// for an empty query block, a query block longer than max_q_len (its rows would not fit
+// the workspace's max_q_len * G rows per head) or a context outside [q_len, max_ctx] (the
+// merge kernel writes such a sequence's rows below max_q_len as zeros and counts it), else
+// its context.
+__device__ __forceinline__ bool mq_bad(int ql, int ctx, int max_q_len, int max_ctx) {
+  return ql > max_q_len || ctx < ql || ctx > max_ctx;
+}
 __device__ __forceinline__ int seq_units(const int32_t* __restrict__ ctx_lens,
-                                         const int32_t* __restrict__ cu_q, int b, int max_ctx) {
+                                         const int32_t* __restrict__ cu_q, int b, int max_ctx,
+                                         int max_q_len) {
   const int ctx = ctx_lens[b];
   if (cu_q == nullptr) return units_of(ctx, max_ctx);
   const int ql = cu_q[b + 1] - cu_q[b];
-  return (ql <= 0 || ctx < ql || ctx > max_ctx) ? 0 : units_of(ctx, max_ctx);
+  return (ql <= 0 || mq_bad(ql, ctx, max_q_len, max_ctx)) ? 0 : units_of(ctx, max_ctx);
 }
 
 // Units of one KV head summed over all sequences (the whole launch is KVH times this).
 __device__ __forceinline__ int64_t head_units(const int32_t* __restrict__ ctx_lens,
                                               const int32_t* __restrict__ cu_q, int B,
-                                              int max_ctx) {
+                                              int max_ctx, int max_q_len) {
   int64_t t = 0;
   for (int b0 = 0; b0 < B; b0 += 64) {
     const int b = b0 + __lane_id();
-    t += wave_sum(b < B ? seq_units(ctx_lens, cu_q, b, max_ctx) : 0);
+    t += wave_sum(b < B ? seq_units(ctx_lens, cu_q, b, max_ctx, max_q_len) : 0);
   }
   return t;
 }
@@ -138,7 +144,8 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
   const int grp = lane >> 4; // lane group: K sub-range of the MFMA operands
 
   // ---- this worker's unit range and where it starts
-  const int64_t C = head_units(ctx_lens, cu_q, B, max_ctx) * NG;
+  const int maxq = RPH / G;  // max_q_len: the workspace's query rows per head / G
+  const int64_t C = head_units(ctx_lens, cu_q, B, max_ctx, maxq) * NG;
   const int64_t W = active_workers(C, num_workers);
   const int64_t w = blockIdx.x;
   if (w >= W) return;
@@ -150,7 +157,7 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
     for (int b0 = 0; b0 < B; b0 += 64) {
       const int bb = b0 + lane;
       const int c = bb < B ? clamp_ctx(ctx_lens[bb], max_ctx) : 0;
-      const int v = bb < B ? seq_units(ctx_lens, cu_q, bb, max_ctx) : 0;
+      const int v = bb < B ? seq_units(ctx_lens, cu_q, bb, max_ctx, maxq) : 0;
       const int incl = wave_incl_scan(v);
       const uint64_t hit = __ballot(int64_t(NG) * (base + incl) > U);
       if (hit) {
@@ -403,7 +410,7 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
       do {
         if (++b >= B) break;
         ctx = clamp_ctx(ctx_lens[b], max_ctx);
-        nb = seq_units(ctx_lens, cu_q, b, max_ctx);
+        nb = seq_units(ctx_lens, cu_q, b, max_ctx, maxq);
       } while (nb == 0);
       if (b >= B) break;
     }
@@ -435,17 +442,18 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
   const int q0 = cu_q ? cu_q[b] : b;
   const int ql = cu_q ? cu_q[b + 1] - q0 : 1;
   if (i >= ql) return;
+  const int maxq = RPH / G;  // max_q_len (the grid's z extent)
   int64_t total = 0, pre = 0;
   for (int b0 = 0; b0 < B; b0 += 64) {
     const int bb = b0 + lane;
-    const int v = bb < B ? seq_units(ctx_lens, cu_q, bb, max_ctx) : 0;
+    const int v = bb < B ? seq_units(ctx_lens, cu_q, bb, max_ctx, maxq) : 0;
     total += wave_sum(v);
     pre += wave_sum(bb < b ? v : 0);
   }
   const int raw = ctx_lens[b];
-  const bool bad = cu_q ? (raw < ql || raw > max_ctx) : (raw < 0 || raw > max_ctx);
+  const bool bad = cu_q ? mq_bad(ql, raw, maxq, max_ctx) : (raw < 0 || raw > max_ctx);
   if (h == 0 && i == 0 && threadIdx.x == 0 && err_count && bad) atomicAdd(err_count, 1);
-  const int nb = seq_units(ctx_lens, cu_q, b, max_ctx);
+  const int nb = seq_units(ctx_lens, cu_q, b, max_ctx, maxq);
   uint16_t* o = out + int64_t(q0 + i) * osb + int64_t(h) * osh;
   if (nb == 0) {
     if (threadIdx.x < D) o[threadIdx.x] = 0;

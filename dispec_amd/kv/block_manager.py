@@ -130,49 +130,54 @@ class BlockManager:
         return child
 
     def cow_fork(self, parent_id: int, child_id: int) -> tuple[BlockTable, list[tuple[int, int]]]:
-        """Fork that copies the parent's partial last block for the child.
+        """Fork that gives the child private copies of every block it may still write.
 
-        Full blocks are shared.  If the parent's last block is partially filled the child
-        gets a private block, and the (src, dst) pair whose data must be copied is
-        returned, so both sequences can append without touching each other's slots.
+        Blocks holding only already-written tokens are shared by refcount.  The parent's
+        partially filled block is copied for the child, and the (src, dst) pair whose data
+        must be moved is returned.  Blocks past the written tokens (room made by `reserve`)
+        hold no data yet, so the child gets fresh private blocks for them with nothing to
+        copy.  Parent and child can then append without touching each other's slots.
         """
         if child_id in self._tables:
             raise ValueError(f"seq {child_id} already allocated")
         parent = self._tables[parent_id]
-        partial = parent.num_tokens % self.block_size != 0
-        last = self.blocks_needed(parent.num_tokens) - 1 if partial else -1
-        if partial and not self._free:
-            raise OutOfBlocksError("block pool exhausted")
-        ids = list(parent.block_ids)
+        written = parent.num_tokens // self.block_size   # blocks holding only written tokens
+        private = len(parent.block_ids) - written          # partial block + reserved room
+        if private > self.num_free_blocks:
+            raise OutOfBlocksError(f"cow_fork needs {private}, have {self.num_free_blocks}")
+        ids = list(parent.block_ids[:written])
+        for blk in ids:
+            self._ref_count[blk] += 1
         copies: list[tuple[int, int]] = []
-        for i, blk in enumerate(ids):
-            if i == last:
-                new = self._alloc_block()
-                copies.append((blk, new))
-                ids[i] = new
-            else:
-                self._ref_count[blk] += 1
+        for i in range(written, len(parent.block_ids)):
+            new = self._alloc_block()
+            if i * self.block_size < parent.num_tokens:      # the partial block: copy it
+                copies.append((parent.block_ids[i], new))
+            ids.append(new)
         child = BlockTable(ids, parent.num_tokens)
         self._tables[child_id] = child
         return child, copies
 
     def ensure_writable(self, seq_id: int) -> list[tuple[int, int]]:
-        """Give the sequence a private copy of its last block if that block is shared.
+        """Give the sequence a private copy of the block its next token goes into.
 
-        Call before writing the next token.  Returns the (src, dst) pair to copy, or []
-        when the next token starts a fresh block or the last block is already private.
+        Call before writing the next token.  When that block exists (partially filled, or
+        reserved ahead) and is shared, it is replaced by a private block.  Returns the
+        (src, dst) pair to copy when the block holds written tokens; [] when the block is
+        already private, does not exist yet (append_token allocates it) or holds none of
+        this sequence's tokens.
         """
         table = self._tables[seq_id]
-        if table.num_tokens % self.block_size == 0 or not table.block_ids:
+        i = table.num_tokens // self.block_size
+        if i >= len(table.block_ids):
             return []
-        i = self.blocks_needed(table.num_tokens) - 1
         blk = table.block_ids[i]
         if self._ref_count[blk] == 1:
             return []
         new = self._alloc_block()
         self._drop(blk)
         table.block_ids[i] = new
-        return [(blk, new)]
+        return [(blk, new)] if table.num_tokens % self.block_size else []
 
     def truncate(self, seq_id: int, num_tokens: int) -> None:
         """Roll back to num_tokens tokens, releasing trailing blocks (spec rejection)."""

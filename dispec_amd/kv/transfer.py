@@ -187,105 +187,136 @@ class LayerMap:
         return self.apply_into(x, [0], K, K, T, out, use_residual)
 
 
+# -- map files and their validation ------------------------------------------------------
+# The on-disk format is kvxfer's (reference loader: dispec/kv/transfer.py:187-230):
+#   maps_dir/maps.json                  {"variants": [...], "source": name, "target": name, ...}
+#   maps_dir/{variant}__{keys|values}.pt  list over target layers of
+#                                       {"source_layers", "bias", "weight" | "factors"}
+#   residual_dir/residual.pt            {"key_residual"|"value_residual":
+#                                        {"{layer}.down.weight", "{layer}.down.bias",
+#                                         "{layer}.up.weight"}}
+# The error and warning texts are the reference's (:151-183, :197-200): callers and tests
+# match on them.
+_RESIDUAL_KEYS = {"keys": "key_residual", "values": "value_residual"}
+_GEOMETRY = (  # (config attribute, how to read it, why a mismatch is fatal)
+    ("num_key_value_heads", lambda c: c.num_key_value_heads,
+     "a source head cannot map onto a target head"),
+    ("head_dim", head_dim_of, "a source head cannot map onto a target head"),
+    ("vocab_size", lambda c: c.vocab_size, "the models do not share a tokenizer"),
+)
+
+
+def _model_name(path: str) -> str:
+    return path.rstrip("/").rpartition("/")[2]
+
+
+def _layer_map_from_state(entry: dict) -> LayerMap:
+    factors = entry.get("factors")
+    return LayerMap(source_layers=tuple(map(int, entry["source_layers"])), bias=entry["bias"],
+                    weight=entry.get("weight"),
+                    factors=None if factors is None else tuple(factors))
+
+
+def _read_stack(path: Path) -> list[LayerMap]:
+    """One kind's per-target-layer maps: entries 0..n-1 of a safe-loaded dict (or list)."""
+    state = torch.load(path, map_location="cpu", weights_only=True)
+    return [_layer_map_from_state(state[i]) for i in range(len(state))]
+
+
+def _stack_problems(kind: str, maps: list[LayerMap], n_src: int, n_tgt: int, kv_dim: int):
+    """Yield the message of every way `maps` cannot produce an n_tgt-layer target."""
+    if len(maps) != n_tgt:
+        yield f"{kind}: {len(maps)} layer maps for a {n_tgt}-layer target"
+        return
+    for layer, m in enumerate(maps):
+        outside = [i for i in m.source_layers if i < 0 or i >= n_src]
+        if outside:
+            yield (f"{kind} map for target layer {layer} reads source layers {outside}, "
+                   f"but the source has {n_src}")
+            continue
+        rows = kv_dim * len(m.source_layers)
+        if m.weight is not None:
+            got = tuple(m.weight.shape)
+        else:
+            got = (m.factors[0].shape[0], m.factors[1].shape[1])
+        if got != (rows, kv_dim) or tuple(m.bias.shape) != (kv_dim,):
+            yield (f"{kind} map for target layer {layer} has shape {got}, "
+                   f"expected {(rows, kv_dim)}")
+        elif m.residual is not None and (m.residual[0].shape[1] != rows
+                                         or m.residual[2].shape[0] != kv_dim):
+            yield (f"{kind} residual for target layer {layer} does not match a "
+                   f"{rows}->{kv_dim} map")
+
+
 class CrossModelKVMap:
     """Maps a source model's contiguous KV (L, T, H, D) into a target model's (:126-283)."""
 
     def __init__(self, keys: list[LayerMap], values: list[LayerMap], source_config,
                  target_config, metadata: dict | None = None):
-        self.keys = keys
-        self.values = values
-        self.metadata = metadata or {}
+        for attr, read, why in _GEOMETRY:
+            a, b = read(source_config), read(target_config)
+            if a != b:
+                raise ValueError(f"cannot transfer KV: {attr} differs ({a} vs {b}); {why}")
+        self.keys, self.values = keys, values
+        self.metadata = dict(metadata or {})
         self.num_kv_heads = target_config.num_key_value_heads
         self.head_dim = head_dim_of(target_config)
-        self.dtype = keys[0].bias.dtype if keys else torch.float32
-        self._check(source_config, target_config)
-
-    def _check(self, source_config, target_config) -> None:
-        src, tgt = source_config, target_config
-        for attr, a, b in (
-            ("num_key_value_heads", src.num_key_value_heads, tgt.num_key_value_heads),
-            ("head_dim", head_dim_of(src), head_dim_of(tgt)),
-            ("vocab_size", src.vocab_size, tgt.vocab_size),
-        ):
-            if a != b:
-                reason = ("the models do not share a tokenizer" if attr == "vocab_size"
-                          else "a source head cannot map onto a target head")
-                raise ValueError(f"cannot transfer KV: {attr} differs ({a} vs {b}); {reason}")
-        n_src, n_tgt = src.num_hidden_layers, tgt.num_hidden_layers
         kv_dim = self.num_kv_heads * self.head_dim
-        for kind, maps in (("keys", self.keys), ("values", self.values)):
-            if len(maps) != n_tgt:
-                raise ValueError(f"{kind}: {len(maps)} layer maps for a {n_tgt}-layer target")
-            for layer, m in enumerate(maps):
-                bad = [s for s in m.source_layers if not 0 <= s < n_src]
-                if bad:
-                    raise ValueError(f"{kind} map for target layer {layer} reads source "
-                                     f"layers {bad}, but the source has {n_src}")
-                design = len(m.source_layers) * kv_dim
-                shape = (m.weight.shape if m.weight is not None
-                         else (m.factors[0].shape[0], m.factors[1].shape[1]))
-                if tuple(shape) != (design, kv_dim) or tuple(m.bias.shape) != (kv_dim,):
-                    raise ValueError(f"{kind} map for target layer {layer} has shape "
-                                     f"{tuple(shape)}, expected {(design, kv_dim)}")
-                if m.residual is not None:
-                    down_w, _, up_w = m.residual
-                    if down_w.shape[1] != design or up_w.shape[0] != kv_dim:
-                        raise ValueError(f"{kind} residual for target layer {layer} does "
-                                         f"not match a {design}->{kv_dim} map")
-        for side, config in (("source", src), ("target", tgt)):
-            recorded = self.metadata.get(side)
-            loaded = getattr(config, "_name_or_path", "") or getattr(config, "name_or_path", "")
-            if recorded and loaded and (recorded.rstrip("/").split("/")[-1]
-                                        != loaded.rstrip("/").split("/")[-1]):
-                warnings.warn(f"maps were fitted with {side} {recorded!r} but {loaded!r} is "
-                              "loaded; geometry matches, quality is not guaranteed", stacklevel=3)
+        for kind, maps in zip(KINDS, (keys, values)):
+            problem = next(_stack_problems(kind, maps, source_config.num_hidden_layers,
+                                           target_config.num_hidden_layers, kv_dim), None)
+            if problem is not None:
+                raise ValueError(problem)
+        self.dtype = keys[0].bias.dtype if keys else torch.float32
+        self._warn_if_other_models(source_config, target_config)
+
+    def _warn_if_other_models(self, source_config, target_config) -> None:
+        """Warn when the configs name other checkpoints than the maps were fitted on."""
+        for side, cfg in (("source", source_config), ("target", target_config)):
+            fitted = self.metadata.get(side) or ""
+            loaded = (getattr(cfg, "_name_or_path", "") or getattr(cfg, "name_or_path", "")
+                      or "")
+            if fitted and loaded and _model_name(fitted) != _model_name(loaded):
+                warnings.warn(f"maps were fitted with {side} {fitted!r} but {loaded!r} is "
+                              "loaded; geometry matches, quality is not guaranteed",
+                              stacklevel=4)
 
     @classmethod
     def load(cls, maps_dir, source_config, target_config, residual_dir=None,
              variant: str = "ridge", device="cuda",
              dtype: torch.dtype = torch.bfloat16) -> "CrossModelKVMap":
         """Read kvxfer's map files (and an optional trained residual) onto the GPU."""
-        maps_dir = Path(maps_dir)
-        manifest = maps_dir / "maps.json"
-        if not manifest.exists():
-            raise FileNotFoundError(f"no maps.json in {maps_dir}")
-        metadata = json.loads(manifest.read_text())
-        if variant not in metadata.get("variants", []):
-            raise ValueError(f"variant {variant!r} not in {metadata.get('variants')}")
-        per_kind = {}
-        for kind in KINDS:
-            state = torch.load(maps_dir / f"{variant}__{kind}.pt", map_location="cpu",
-                               weights_only=True)
-            layers = []
-            for layer in range(len(state)):
-                s = state[layer]
-                factors = s.get("factors")
-                layers.append(LayerMap(
-                    source_layers=tuple(int(i) for i in s["source_layers"]), bias=s["bias"],
-                    weight=s.get("weight"),
-                    factors=tuple(factors) if factors is not None else None))
-            per_kind[kind] = layers
+        root = Path(maps_dir)
+        try:
+            manifest = json.loads((root / "maps.json").read_text())
+        except FileNotFoundError:
+            raise FileNotFoundError(f"no maps.json in {root}") from None
+        offered = manifest.get("variants", [])
+        if variant not in offered:
+            raise ValueError(f"variant {variant!r} not in {manifest.get('variants')}")
+        stacks = {kind: _read_stack(root / f"{variant}__{kind}.pt") for kind in KINDS}
         if residual_dir is not None:
-            res = torch.load(Path(residual_dir) / "residual.pt", map_location="cpu",
-                             weights_only=True)
-            for kind, key in (("keys", "key_residual"), ("values", "value_residual")):
-                sd = res[key]
-                for layer, m in enumerate(per_kind[kind]):
-                    m.residual = (sd[f"{layer}.down.weight"], sd[f"{layer}.down.bias"],
-                                  sd[f"{layer}.up.weight"])
-        kv_map = cls(per_kind["keys"], per_kind["values"], source_config, target_config,
-                     metadata)
-        return kv_map.to(device, dtype)
+            trained = torch.load(Path(residual_dir) / "residual.pt", map_location="cpu",
+                                 weights_only=True)
+            for kind, maps in stacks.items():
+                sd = trained[_RESIDUAL_KEYS[kind]]
+                for i, m in enumerate(maps):
+                    m.residual = tuple(sd[f"{i}.{part}"] for part in
+                                       ("down.weight", "down.bias", "up.weight"))
+        return cls(stacks["keys"], stacks["values"], source_config, target_config,
+                   manifest).to(device, dtype)
 
     def to(self, device, dtype: torch.dtype) -> "CrossModelKVMap":
-        for m in (*self.keys, *self.values):
+        """Move every layer map to `device` / `dtype` (done once, at load)."""
+        for m in self.keys + self.values:
             m.to(device, dtype)
         self.dtype = dtype
         return self
 
     @property
     def has_residual(self) -> bool:
-        return self.keys[0].residual is not None
+        """Whether trained residual maps are attached (decided by the first key map)."""
+        return bool(self.keys) and self.keys[0].residual is not None
 
     def _apply(self, source: torch.Tensor, maps: list[LayerMap], use_residual: bool,
                rope: tuple[torch.Tensor, torch.Tensor] | None = None,

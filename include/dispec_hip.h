@@ -185,7 +185,11 @@ int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  *   q, out     : packed [sum q_len, Hq, D], strides (q_stride_t, q_stride_h).
  *   block_table: int32 [B, bt_stride] (power-of-two block_size).
  *   cu_q       : int32 [B+1] device offsets; ctx_lens: int32 [B], q_len_b <= ctx <= max_ctx.
- *   max_q_len  : upper bound of q_len_b (sizes the grid).
+ *   max_q_len  : upper bound of q_len_b (sizes the grid and the workspace).  A larger
+ *                q_len_b is a caller error that never leads to an out-of-bounds access:
+ *                the balanced split counts it in err_count and writes the sequence's first
+ *                max_q_len query rows as zeros; the tiled kernels compute only the rows
+ *                their max_q_len-sized grid covers.
  *   partition_tokens : split-K key partition (multiple of 128, at most 64 partitions of
  *                max_ctx); 0 picks one from the shape.  More than one partition needs
  *                `workspace` (dsp_paged_mq_workspace_bytes with the same partition_tokens,

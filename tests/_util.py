@@ -58,3 +58,46 @@ def random_block_tables(num_blocks: int, lens, block_size: int, seed: int) -> li
         at += need
     assert at <= num_blocks, "pool too small for the requested lengths"
     return tables
+
+
+# ------------------------------------------------------------ bf16 rounding-chain bounds
+def bf16_spacing(x) -> np.ndarray:
+    """Gap between adjacent bf16 values at magnitude |x| (8 significand bits): 2^(e-7)
+    for |x| in [2^e, 2^(e+1)); 0 where x == 0."""
+    m = np.abs(np.asarray(x, np.float64))
+    e = np.floor(np.log2(np.where(m > 0, m, 1.0)))
+    return np.where(m > 0, np.exp2(e - 7), 0.0)
+
+
+def bf16_chain_bound(*stages, lipschitz: float = 1.0) -> np.ndarray:
+    """Per-element bound on |got - ref| for two evaluations of one chain of bf16 roundings
+    whose exact inputs agree up to fp32 accumulation order.
+
+    `stages` are (upper bounds of) the magnitudes of the value rounded at each step, in
+    order.  Two roundings of values that differ by e land at most e + one gap apart, and
+    the gap at the next binade up is twice the gap at |x|, so each step adds 2 gaps at its
+    magnitude; `lipschitz` bounds how much a step between roundings (e.g. gelu, |f'| <
+    1.13) can amplify the error carried into it.
+    """
+    bound = 0.0
+    for m in stages:
+        bound = lipschitz * bound + 2.0 * bf16_spacing(np.asarray(m, np.float64) * (1 + 2 ** -7))
+    return bound
+
+
+def assert_bf16_within(got_bits, ref_bits, bound, what, min_exact: float = 0.99) -> None:
+    """Every element within its own `bound` of the reference, and at least `min_exact` of
+    the elements bit-identical (a differing bit pattern is a rounding-boundary case)."""
+    from oracle import ref_cpu
+    got_bits, ref_bits = np.asarray(got_bits, np.uint16), np.asarray(ref_bits, np.uint16)
+    got = ref_cpu.bf16_to_f32(got_bits).astype(np.float64)
+    ref = ref_cpu.bf16_to_f32(ref_bits).astype(np.float64)
+    err = np.abs(got - ref)
+    bound = np.broadcast_to(np.asarray(bound, np.float64), err.shape)
+    over = err > bound
+    exact = float((got_bits == ref_bits).mean()) if got.size else 1.0
+    if over.any():
+        i = np.unravel_index(int(np.argmax(err - bound)), err.shape)
+        raise AssertionError(f"{what}: {int(over.sum())} elements outside their bound; worst "
+                             f"at {i}: got {got[i]:.6g} ref {ref[i]:.6g} bound {bound[i]:.3g}")
+    assert exact >= min_exact, f"{what}: only {exact:.4f} of outputs bit-identical"

@@ -116,3 +116,57 @@ def test_ensure_writable_after_refcount_fork():
     bm.free(1)
     bm.free(2)
     assert bm.num_free_blocks == 10
+
+
+def _slots_after_appends(bm, seq, n):
+    return [bm.append_token(seq) for _ in range(n)]
+
+
+def test_cow_fork_after_reserve_gives_private_room():
+    # 20 tokens in blocks of 16, room reserved for 14 more (a third block), then a fork:
+    # the partial block is copied, the reserved block is the child's own (nothing to copy)
+    bm = BlockManager(num_blocks=20, block_size=16)
+    bm.allocate(0, 20)
+    bm.reserve(0, 14)
+    parent = bm.block_table(0)
+    assert len(parent.block_ids) == 3
+    child, pairs = bm.cow_fork(0, 1)
+    assert pairs == [(parent.block_ids[1], child.block_ids[1])]
+    assert child.block_ids[0] == parent.block_ids[0]
+    assert child.block_ids[2] != parent.block_ids[2]
+    assert bm.ref_count(parent.block_ids[0]) == 2 and bm.ref_count(parent.block_ids[2]) == 1
+    # 13 appends each: the 13th crosses into the reserved block; no slot is shared
+    a = _slots_after_appends(bm, 0, 13)
+    b = _slots_after_appends(bm, 1, 13)
+    assert not set(a) & set(b)
+    bm.free(0)
+    bm.free(1)
+    assert bm.num_free_blocks == 20
+
+
+def test_ensure_writable_unshares_a_reserved_block():
+    # a reference-style fork shares the reserved block too; ensure_writable un-shares the
+    # block the next token goes into, with a copy only when it holds written tokens
+    bm = BlockManager(num_blocks=20, block_size=16)
+    bm.allocate(0, 32)
+    bm.reserve(0, 5)
+    bm.fork(0, 1)
+    reserved = bm.block_table(0).block_ids[2]
+    assert bm.ensure_writable(1) == []            # next token opens the reserved block
+    assert bm.block_table(1).block_ids[2] != reserved
+    assert bm.ref_count(reserved) == 1
+    assert bm.append_token(0)[0] == reserved
+    assert bm.append_token(1)[0] == bm.block_table(1).block_ids[2]
+    # a partially written shared block is copied
+    bm.fork(0, 2)
+    pairs = bm.ensure_writable(2)
+    assert pairs == [(reserved, bm.block_table(2).block_ids[2])]
+
+
+def test_cow_fork_out_of_blocks_counts_reserved_room():
+    bm = BlockManager(num_blocks=4, block_size=4)
+    bm.allocate(0, 6)          # full + partial
+    bm.reserve(0, 6)           # + 1 reserved -> 3 blocks, 1 free
+    with pytest.raises(OutOfBlocksError):
+        bm.cow_fork(0, 1)      # needs the partial copy and the reserved block: 2
+    assert not bm.has_table(1) and bm.num_free_blocks == 1

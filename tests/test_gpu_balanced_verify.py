@@ -136,6 +136,37 @@ def test_bad_lengths_are_counted_once_and_zeroed():
     assert_attention_close(o[keep], ref[keep], "good sequences beside bad ones")
 
 
+def test_query_block_longer_than_max_q_len_is_counted_and_stays_in_bounds():
+    """A caller passing max_q_len below a sequence's real q_len: that sequence is counted
+    once, its first max_q_len query rows are zeros and its later rows untouched, the other
+    sequences are right, and nothing past the workspace is written."""
+    from dispec_amd import _lib
+    from dispec_amd.engine.hip_attn import paged_mq_attention
+    q_lens, ctx = [5, 8, 3, 5], [300, 500, 100, 2000]          # seq 1: q_len 8 > 5
+    Hq, KVH, D, G, maxq = 16, 8, 128, 2, 5
+    q, kc, vc, bt, cu, tables = _inputs(q_lens, ctx, Hq, KVH, D, 775)
+    need = _lib.lib().dsp_paged_mq_workspace_bytes(len(ctx), Hq, KVH, D, maxq,
+                                                    bt.shape[1] * 16, _lib.DSP_SPLIT_BALANCED)
+    words = need // 4 + 1
+    ws = torch.full((words + 4096,), 12345.0, dtype=torch.float32, device=DEV)
+    out = torch.full((sum(q_lens), Hq, D), 7.0, dtype=torch.bfloat16, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    paged_mq_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), cu.to(DEV),
+                       torch.tensor(ctx, dtype=torch.int32).to(DEV), G, max_q_len=maxq,
+                       max_ctx=bt.shape[1] * 16, err=err, balanced=True, out=out,
+                       workspace=ws[:words])
+    torch.cuda.synchronize()
+    assert int(err.item()) == 1
+    assert bool((ws[words:] == 12345.0).all()), "workspace guard overwritten"
+    o = f64(out)
+    assert not np.any(o[5:10]), "rows of the first max_q_len queries must be zeros"
+    assert np.all(o[10:13] == 7.0), "rows past max_q_len must be left untouched"
+    slots = [ref_cpu.context_slots(t, n, 16) for t, n in zip(tables, ctx)]
+    ref = ref_cpu.mq_attention(f64(q), f64(kc), f64(vc), slots, q_lens, G)
+    keep = np.r_[0:5, 13:21]
+    assert_attention_close(o[keep], ref[keep], "good sequences beside an over-long block")
+
+
 def test_rejects_unsupported_shapes(hip):
     """The balanced split needs max_q_len * G <= 16 and excludes a shared prefix."""
     from dispec_amd.engine.hip_attn import paged_mq_attention

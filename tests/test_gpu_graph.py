@@ -19,7 +19,7 @@ import pytest
 import torch
 
 from oracle import ref_torch
-from tests.tiny_models import tiny_qwen2, tiny_qwen3
+from tests.toy_lm import toy_lm
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -30,7 +30,7 @@ BLOCKS_PER_SEQ = 8          # 128 tokens per sequence
 def _setup(family="qwen3", num_seqs=4):
     from dispec_amd.engine.model_runner import ModelRunner
     from dispec_amd.kv.paged_cache import PagedKVCache
-    base = (tiny_qwen3 if family == "qwen3" else tiny_qwen2)().to(torch.bfloat16)
+    base = toy_lm(family).to(torch.bfloat16)
     cpu = copy.deepcopy(base).float()
     gm = base.to(DEV)
     runner = ModelRunner(gm, attn_backend="hip")

@@ -14,15 +14,15 @@ import pytest
 import torch
 
 from oracle import ref_torch
-from tests.tiny_models import tiny_qwen2, tiny_qwen3
+from tests.toy_lm import toy_lm
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-MODELS = {"qwen3": tiny_qwen3, "qwen2": tiny_qwen2}
+FAMILIES = ("qwen3", "qwen2")
 
 
 def _pair(family):
-    base = MODELS[family]().to(torch.bfloat16)
+    base = toy_lm(family).to(torch.bfloat16)
     ref = copy.deepcopy(base).float()          # same bf16-rounded weights, fp32 math
     return base.to(DEV), ref
 
@@ -71,7 +71,7 @@ def _cos(a, b):
     return torch.nn.functional.cosine_similarity(a, b, dim=-1)
 
 
-@pytest.mark.parametrize("family", sorted(MODELS))
+@pytest.mark.parametrize("family", sorted(FAMILIES))
 def test_prefill_then_decode_matches_native(family):
     gm, cm = _pair(family)
     both = _Both(gm, cm)
@@ -86,7 +86,7 @@ def test_prefill_then_decode_matches_native(family):
         nxt, cur = int(ref[0].argmax()), cur + 1
 
 
-@pytest.mark.parametrize("family", sorted(MODELS))
+@pytest.mark.parametrize("family", sorted(FAMILIES))
 def test_chunked_prefill_and_mixed_batch(family):
     gm, cm = _pair(family)
     both = _Both(gm, cm)
@@ -166,7 +166,7 @@ def test_decode_of_forked_sequences_uses_the_shared_prefix():
         cur += 1
 
 
-@pytest.mark.parametrize("family", sorted(MODELS))
+@pytest.mark.parametrize("family", sorted(FAMILIES))
 def test_verify_of_skewed_sequences_uses_the_balanced_split(family):
     """A 5-token verify over sequences of 600, 20, 45 and 9 tokens (independent prompts,
     no shared blocks): the runner picks the balanced split-K kernel (its keys per resident
@@ -191,4 +191,4 @@ def test_verify_of_skewed_sequences_uses_the_balanced_split(family):
 def test_rejects_other_backends():
     from dispec_amd.engine.model_runner import ModelRunner
     with pytest.raises(ValueError, match="hip"):
-        ModelRunner(tiny_qwen3(), attn_backend="triton")
+        ModelRunner(toy_lm("qwen3"), attn_backend="triton")

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from oracle import ref_torch
-from tests.tiny_models import tiny_qwen2, tiny_qwen3
+from tests.toy_lm import toy_lm
 
 
 def _pool(model, nb=16, bs=16):
@@ -18,9 +18,9 @@ def _pool(model, nb=16, bs=16):
     return torch.zeros(shape), torch.zeros(shape)
 
 
-@pytest.mark.parametrize("make", [tiny_qwen3, tiny_qwen2])
-def test_native_forward_matches_hf(make):
-    model = make()
+@pytest.mark.parametrize("family", ["qwen3", "qwen2"])
+def test_native_forward_matches_hf(family):
+    model = toy_lm(family)
     ids = torch.randint(0, 128, (37,), generator=torch.Generator().manual_seed(3))
     key, value = _pool(model)
     blocks = [5, 9, 2]
@@ -34,7 +34,7 @@ def test_native_forward_matches_hf(make):
 
 
 def test_native_forward_chunked_equals_whole():
-    model = tiny_qwen3()
+    model = toy_lm("qwen3")
     ids = torch.randint(0, 128, (40,), generator=torch.Generator().manual_seed(1))
     blocks = [3, 7, 1]
     key, value = _pool(model)

@@ -1,12 +1,13 @@
-"""Map files, validation and host-side behaviour of dispec_amd.kv.transfer (CPU only).
+"""Host side of dispec_amd.kv.transfer on the CPU: kvxfer's map-file format, validation and
+the GPU-only guard of the apply path.
 
-Restates the reference's CPU tests of the file format and validation
-(tests/test_kv_transfer.py:79-87, :138-182) against dispec_amd's loader.  Loading with
-device="cpu" runs only host code; applying a map needs the GPU and must say so.
+The format (maps.json + {variant}__{keys|values}.pt + residual/residual.pt) and the error
+texts are what the reference's loader reads and raises (dispec/kv/transfer.py:144-230);
+the reference's own CPU tests of them are tests/test_kv_transfer.py:79-87, :138-182.
+Loading with device="cpu" runs only host code; applying a map needs the GPU.
 """
 
 import json
-from pathlib import Path
 from types import SimpleNamespace
 
 import pytest
@@ -14,106 +15,188 @@ import torch
 
 from dispec_amd.kv.transfer import CrossModelKVMap
 
-H, D = 2, 4
-KV_DIM = H * D
+HEADS, HEAD_DIM = 2, 4
+KV = HEADS * HEAD_DIM
 
 
-def _config(n_layers, vocab=100, heads=H, head_dim=D, name="org/model"):
-    return SimpleNamespace(num_hidden_layers=n_layers, num_key_value_heads=heads,
-                           head_dim=head_dim, hidden_size=16, num_attention_heads=4,
+def model_config(layers, *, name, vocab=64, heads=HEADS, head_dim=HEAD_DIM):
+    return SimpleNamespace(num_hidden_layers=layers, num_key_value_heads=heads,
+                           head_dim=head_dim, hidden_size=32, num_attention_heads=8,
                            vocab_size=vocab, _name_or_path=name)
 
 
-def _write_maps(path: Path, n_src, n_tgt, k=2, seed=0, source="org/src", target="org/tgt"):
-    """A map directory in kvxfer's save_maps format (tests/test_kv_transfer.py:49-62)."""
-    g = torch.Generator().manual_seed(seed)
-    for kind in ("keys", "values"):
-        state = {}
-        for t in range(n_tgt):
-            layers = sorted(torch.randperm(n_src, generator=g)[:k].tolist())
-            state[t] = {"weight": torch.randn(k * KV_DIM, KV_DIM, generator=g),
-                        "bias": torch.randn(KV_DIM, generator=g), "source_layers": layers,
-                        "target_layer": t, "r2": 0.5, "rank": None, "factors": None}
-        torch.save(state, path / f"ridge__{kind}.pt")
-    (path / "maps.json").write_text(json.dumps(
-        {"source": source, "target": target, "variants": ["ridge"]}))
-    return path
+class MapFiles:
+    """Writes a map directory the way kvxfer's save_maps lays it out.
+
+    Layer t of either kind reads source layers `sources(t)`; layers listed in `factored`
+    are stored as low-rank (left, right) factors instead of a dense weight.  Every tensor
+    is filled with distinct values so a mix-up between layers or kinds is visible.
+    """
+
+    def __init__(self, root, n_src, n_tgt, *, fan_in=2, factored=(), rank=3,
+                 fitted=("team/src-model", "team/tgt-model"), variants=("ridge",)):
+        self.root, self.n_src, self.n_tgt = root, n_src, n_tgt
+        self.fan_in, self.factored, self.rank = fan_in, set(factored), rank
+        self.fitted, self.variants = fitted, variants
+        self.saved = {}
+
+    def sources(self, t):
+        return [(t + j) % self.n_src for j in range(self.fan_in)]
+
+    def _tensor(self, *shape, tag):
+        n = 1
+        for d in shape:
+            n *= d
+        return (torch.arange(n, dtype=torch.float32).reshape(shape) / 64 + tag)
+
+    def write(self, variant="ridge", weight_rows=None, bias_len=KV):
+        for kid, kind in enumerate(("keys", "values")):
+            entries = {}
+            for t in range(self.n_tgt):
+                rows = weight_rows or self.fan_in * KV
+                tag = 10 * kid + t
+                e = {"source_layers": self.sources(t), "target_layer": t,
+                     "bias": self._tensor(bias_len, tag=-tag), "r2": 0.9}
+                if t in self.factored:
+                    e["weight"], e["rank"] = None, self.rank
+                    e["factors"] = (self._tensor(rows, self.rank, tag=tag),
+                                    self._tensor(self.rank, KV, tag=tag + 0.5))
+                else:
+                    e["weight"], e["rank"], e["factors"] = self._tensor(rows, KV, tag=tag), None, None
+                entries[t] = e
+            torch.save(entries, self.root / f"{variant}__{kind}.pt")
+            self.saved[kind] = entries
+        self.root.joinpath("maps.json").write_text(json.dumps(
+            {"source": self.fitted[0], "target": self.fitted[1],
+             "variants": list(self.variants)}))
+        return self
+
+    def write_residual(self, hidden=5, design=None):
+        design = design or self.fan_in * KV
+        out = self.root / "residual"
+        out.mkdir(exist_ok=True)
+        state = {"hidden": hidden, "design_dim": design}
+        for kid, key in enumerate(("key_residual", "value_residual")):
+            state[key] = {}
+            for t in range(self.n_tgt):
+                tag = 100 + 10 * kid + t
+                state[key][f"{t}.down.weight"] = self._tensor(hidden, design, tag=tag)
+                state[key][f"{t}.down.bias"] = self._tensor(hidden, tag=-tag)
+                state[key][f"{t}.up.weight"] = self._tensor(KV, hidden, tag=tag + 0.25)
+        torch.save(state, out / "residual.pt")
+        self.residual = state
+        return out
+
+    def load(self, src=None, tgt=None, **kw):
+        src = src or model_config(self.n_src, name="team/src-model")
+        tgt = tgt or model_config(self.n_tgt, name="team/tgt-model")
+        return CrossModelKVMap.load(self.root, src, tgt, device="cpu", **kw)
 
 
-def _load(path, n_src, n_tgt, **kw):
-    return CrossModelKVMap.load(path, _config(n_src, name="org/src"),
-                                _config(n_tgt, name="org/tgt"), device="cpu", **kw)
+def bf16(t):
+    return t.to(torch.bfloat16)
 
 
-def test_load_reads_kvxfer_map_format(tmp_path):
-    _write_maps(tmp_path, n_src=3, n_tgt=4)
-    kv_map = _load(tmp_path, 3, 4)
-    saved = torch.load(tmp_path / "ridge__keys.pt", weights_only=True)
-    assert len(kv_map.keys) == len(kv_map.values) == 4
-    assert kv_map.dtype == torch.bfloat16
-    for t, m in enumerate(kv_map.keys):
-        assert m.source_layers == tuple(saved[t]["source_layers"])
-        torch.testing.assert_close(m.weight, saved[t]["weight"].to(torch.bfloat16))
+def test_every_layer_of_both_kinds_loads_as_written(tmp_path):
+    files = MapFiles(tmp_path, n_src=5, n_tgt=4, factored=(1, 3)).write()
+    kv_map = files.load()
+    assert kv_map.dtype == torch.bfloat16 and not kv_map.has_residual
+    for kind, loaded in (("keys", kv_map.keys), ("values", kv_map.values)):
+        assert len(loaded) == 4
+        for t, m in enumerate(loaded):
+            want = files.saved[kind][t]
+            assert m.source_layers == tuple(files.sources(t))
+            assert torch.equal(m.bias, bf16(want["bias"]))
+            if t in files.factored:
+                assert m.weight is None
+                assert all(torch.equal(a, bf16(b)) for a, b in zip(m.factors, want["factors"]))
+            else:
+                assert m.factors is None and torch.equal(m.weight, bf16(want["weight"]))
 
 
-def test_residual_loads_from_kvxfer_format(tmp_path):
-    _write_maps(tmp_path, n_src=3, n_tgt=2)
-    hidden, design = 5, 2 * KV_DIM
-    sd = lambda: {f"{i}.{name}": torch.randn(shape)  # noqa: E731
-                  for i in range(2) for name, shape in
-                  (("down.weight", (hidden, design)), ("down.bias", (hidden,)),
-                   ("up.weight", (KV_DIM, hidden)))}
-    res = tmp_path / "residual"
-    res.mkdir()
-    state = {"key_residual": sd(), "value_residual": sd(), "hidden": hidden, "design_dim": design}
-    torch.save(state, res / "residual.pt")
-    kv_map = _load(tmp_path, 3, 2, residual_dir=res)
+def test_load_honours_dtype(tmp_path):
+    kv_map = MapFiles(tmp_path, 3, 2).write().load(dtype=torch.float32)
+    assert kv_map.dtype == torch.float32
+    assert all(m.weight.dtype == torch.float32 for m in kv_map.keys + kv_map.values)
+
+
+def test_residual_attaches_to_the_right_layer_and_kind(tmp_path):
+    files = MapFiles(tmp_path, n_src=3, n_tgt=3).write()
+    kv_map = files.load(residual_dir=files.write_residual())
     assert kv_map.has_residual
-    torch.testing.assert_close(kv_map.values[1].residual[2],
-                               state["value_residual"]["1.up.weight"].to(torch.bfloat16))
+    for kind, key in (("keys", "key_residual"), ("values", "value_residual")):
+        for t, m in enumerate(getattr(kv_map, kind)):
+            sd = files.residual[key]
+            for got, part in zip(m.residual, ("down.weight", "down.bias", "up.weight")):
+                assert torch.equal(got, bf16(sd[f"{t}.{part}"]))
 
 
-def test_missing_manifest_and_variant(tmp_path):
-    with pytest.raises(FileNotFoundError, match="maps.json"):
-        _load(tmp_path, 3, 2)
-    _write_maps(tmp_path, 3, 2)
-    with pytest.raises(ValueError, match="variant 'lasso'"):
-        _load(tmp_path, 3, 2, variant="lasso")
+@pytest.mark.parametrize("case", ["no manifest", "unknown variant"])
+def test_missing_files_are_named(tmp_path, case):
+    if case == "no manifest":
+        with pytest.raises(FileNotFoundError, match="no maps.json in"):
+            MapFiles(tmp_path, 3, 2).load()
+    else:
+        MapFiles(tmp_path, 3, 2, variants=("ridge", "lowrank")).write()
+        with pytest.raises(ValueError, match=r"variant 'pca' not in \['ridge', 'lowrank'\]"):
+            MapFiles(tmp_path, 3, 2).load(variant="pca")
 
 
-def test_rejects_models_without_a_shared_tokenizer(tmp_path):
-    _write_maps(tmp_path, 3, 2)
-    with pytest.raises(ValueError, match="tokenizer"):
-        CrossModelKVMap.load(tmp_path, _config(3), _config(2, vocab=101), device="cpu")
+GEOMETRY_CASES = {
+    "vocab": (dict(vocab=65), {}, "vocab_size differs .* do not share a tokenizer"),
+    "head_dim": ({}, dict(head_dim=8), "head_dim differs .*cannot map onto a target head"),
+    "kv_heads": (dict(heads=4), {}, "num_key_value_heads differs"),
+}
 
 
-def test_rejects_mismatched_kv_geometry(tmp_path):
-    _write_maps(tmp_path, 3, 2)
-    with pytest.raises(ValueError, match="head_dim"):
-        CrossModelKVMap.load(tmp_path, _config(3, head_dim=8), _config(2), device="cpu")
-    with pytest.raises(ValueError, match="num_key_value_heads"):
-        CrossModelKVMap.load(tmp_path, _config(3, heads=4), _config(2), device="cpu")
+@pytest.mark.parametrize("case", sorted(GEOMETRY_CASES))
+def test_models_that_cannot_exchange_kv_are_rejected(tmp_path, case):
+    src_kw, tgt_kw, msg = GEOMETRY_CASES[case]
+    files = MapFiles(tmp_path, 3, 2).write()
+    with pytest.raises(ValueError, match="cannot transfer KV: " + msg):
+        files.load(src=model_config(3, name="a/s", **src_kw),
+                   tgt=model_config(2, name="a/t", **tgt_kw))
 
 
-def test_rejects_maps_that_do_not_fit_the_models(tmp_path):
-    _write_maps(tmp_path, n_src=3, n_tgt=2)
-    with pytest.raises(ValueError, match="2 layer maps for a 3-layer target"):
-        CrossModelKVMap.load(tmp_path, _config(3), _config(3), device="cpu")
-    with pytest.raises(ValueError, match="source has 1"):
-        CrossModelKVMap.load(tmp_path, _config(1), _config(2), device="cpu")
+def test_maps_that_do_not_fit_the_models_are_rejected(tmp_path):
+    files = MapFiles(tmp_path, n_src=4, n_tgt=2, fan_in=2).write()
+    with pytest.raises(ValueError, match="keys: 2 layer maps for a 5-layer target"):
+        files.load(tgt=model_config(5, name="team/tgt-model"))
+    # target layer 1 reads source layers 1 and 2; a 2-layer source lacks layer 2
+    with pytest.raises(ValueError, match=r"target layer 1 reads source layers \[2\], "
+                                         "but the source has 2"):
+        files.load(src=model_config(2, name="team/src-model"))
+    files.write(weight_rows=3 * KV)
+    with pytest.raises(ValueError, match=r"keys map for target layer 0 has shape \(24, 8\), "
+                                         r"expected \(16, 8\)"):
+        files.load()
+    files.write(bias_len=KV + 1)
+    with pytest.raises(ValueError, match="has shape"):
+        files.load()
+    files.write()
+    with pytest.raises(ValueError, match="residual for target layer 0 does not match a "
+                                         "16->8 map"):
+        files.load(residual_dir=files.write_residual(design=3 * KV))
 
 
-def test_warns_when_maps_were_fitted_for_other_models(tmp_path):
-    _write_maps(tmp_path, 3, 2, source="org/other")
-    with pytest.warns(UserWarning, match="fitted with source"):
-        CrossModelKVMap.load(tmp_path, _config(3, name="org/src"), _config(2, name="org/tgt"),
-                             device="cpu")
+@pytest.mark.parametrize("side", ["source", "target"])
+def test_maps_fitted_for_other_checkpoints_warn(tmp_path, side):
+    fitted = {"source": ("team/other", "team/tgt-model"),
+              "target": ("team/src-model", "team/other")}[side]
+    files = MapFiles(tmp_path, 3, 2, fitted=fitted).write()
+    with pytest.warns(UserWarning, match=f"maps were fitted with {side} 'team/other'"):
+        files.load()
 
 
-def test_map_needs_the_gpu(tmp_path):
-    _write_maps(tmp_path, 3, 2)
-    kv_map = _load(tmp_path, 3, 2)
-    k = torch.zeros(3, 5, H, D)
-    rope = (torch.ones(5, D), torch.zeros(5, D))
+def test_same_checkpoint_under_another_directory_does_not_warn(tmp_path, recwarn):
+    MapFiles(tmp_path, 3, 2, fitted=("hub/src-model", "/data/ckpt/tgt-model/")).write()
+    MapFiles(tmp_path, 3, 2).load()
+    assert not [w for w in recwarn if "fitted with" in str(w.message)]
+
+
+def test_applying_a_map_requires_the_gpu(tmp_path):
+    kv_map = MapFiles(tmp_path, 3, 2).write().load()
+    k = torch.zeros(3, 5, HEADS, HEAD_DIM)
+    rope = (torch.ones(5, HEAD_DIM), torch.zeros(5, HEAD_DIM))
     with pytest.raises(RuntimeError, match="GPU only"):
         kv_map.map(k, k, rope, rope)
