@@ -16,14 +16,18 @@ Reported beside it on the same JSON line:
                 launch time from HIP events on the launch stream, against 8 TB/s; beside
                 it two read ceilings measured in the same run (a streaming read, and the
                 decode's access pattern with no arithmetic: dsp_probe_*)
-  cpu_baseline  the reference's CPU torch path (gather + repeat_interleave + SDPA) on a
-                bounded sample of the same workload, timed on this host
+  cpu_baseline  the reference's CPU torch path (gather + repeat_interleave + SDPA) on one
+                whole layer of the same workload -- the GPU run's own tensors -- timed on
+                this host's cores (median of 5)
   aux           the other configurations, each timed kernel-only with device-resident
                 tables: config 2 (decode step), config 4 (copy-on-write fork, suffix
                 append, 5-query verify, evict-by-copy), config 5 (gather, map GEMM,
                 scatter), a prefill-scale append, skewed decode batches (one long
                 context among short ones) with the balanced and the fixed split, and the
-                measured streaming-copy ceiling the byte-moving kernels are bounded by
+                measured streaming-copy ceiling the byte-moving kernels are bounded by.
+                The byte movers (copy-on-write, appends, evict, gather, scatter) are timed
+                cold -- a 1 GiB fill evicts the L2s and the 256 MB Infinity Cache before
+                each call -- with the warm figure beside (`*_warm_GBps`)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-aux]
 """
@@ -61,6 +65,32 @@ def _fill_randn(torch, t, seed: int) -> None:
         t[i].normal_(generator=g)
 
 
+_PROBE = None
+
+
+def _probe_lib():
+    """libdispec_probe.so: the bandwidth probes (dispec_amd/probe/dsp_probe.h), built beside
+    the product library but not part of it."""
+    global _PROBE
+    if _PROBE is None:
+        import ctypes
+        from ctypes import c_int, c_int32, c_int64, c_void_p
+        path = os.path.join(ROOT, "dispec_amd", "libdispec_probe.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built; run `python -m dispec_amd.build` first")
+        lib = ctypes.CDLL(path)
+        P = c_void_p
+        sigs = {"dsp_probe_stream_read": [P, c_int64, c_int32, P, P],
+                "dsp_probe_stream_copy": [P, P, c_int64, c_int32, P],
+                "dsp_probe_slice_read": [P, P, c_int64, P, c_int64, c_int32, c_int32, c_int32,
+                                         c_int32, c_int32, P, P]}
+        for name, args in sigs.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = c_int, args
+        _PROBE = lib
+    return _PROBE
+
+
 def _time_gpu(torch, fn, iters: int, warmup: int = 2) -> float:
     """Average seconds per call of fn, HIP events on torch's current stream."""
     for _ in range(warmup):
@@ -75,8 +105,31 @@ def _time_gpu(torch, fn, iters: int, warmup: int = 2) -> float:
     return a.elapsed_time(b) / iters / 1e3
 
 
+_FLUSH = None
+
+
+def _time_gpu_cold(torch, fn, iters: int, warmup: int = 1) -> float:
+    """Average seconds per call of fn with the caches cold: before each call a 1 GiB fill
+    evicts the L2s and the 256 MB Infinity Cache (MALL), and HIP events bracket fn alone.
+    The fill is enqueued ahead of fn, so the GPU stays busy while the host launches fn."""
+    global _FLUSH
+    if _FLUSH is None:
+        _FLUSH = torch.empty(1 << 28, dtype=torch.float32, device="cuda")
+    for _ in range(warmup):
+        fn()
+    ev = [_events(torch) for _ in range(iters)]
+    torch.cuda.synchronize()
+    for a, b in ev:
+        _FLUSH.fill_(1.0)
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ev) / iters / 1e3
+
+
 # ------------------------------------------------------------------------------ config 3
-def bench_decode(torch, steps: int, warmup: int) -> dict:
+def bench_decode(torch, steps: int, warmup: int, keep_cpu_sample: bool = False) -> dict:
     from dispec_amd import _lib
     from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
     from dispec_amd.kv.paged_cache import PagedKVCache
@@ -145,13 +198,14 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
     span = cache.key[0:2]
+    probe = _probe_lib()
 
     def stream_probe():
-        _lib.check(lib.dsp_probe_stream_read(span.data_ptr(), span.numel() * 2, 8192,
+        _lib.check(probe.dsp_probe_stream_read(span.data_ptr(), span.numel() * 2, 8192,
                                              sink.data_ptr(), stream), "probe")
 
     def slice_probe(waves):
-        _lib.check(lib.dsp_probe_slice_read(cache.key[0].data_ptr(), cache.value[0].data_ptr(),
+        _lib.check(probe.dsp_probe_slice_read(cache.key[0].data_ptr(), cache.value[0].data_ptr(),
                                             cache.key.shape[1], bt.data_ptr(), bt.stride(0), bs,
                                             B, KVH, ctx, waves, sink.data_ptr(), stream), "probe")
     stream_s = _time_gpu(torch, stream_probe, 10)
@@ -171,45 +225,48 @@ def bench_decode(torch, steps: int, warmup: int) -> dict:
         fixed_ms.extend(e[0].elapsed_time(e[1]) for e in ev)
     cache.check_errors()
     fixed_s = statistics.mean(fixed_ms) / 1e3
+    if keep_cpu_sample:
+        # layer 0 exactly as the GPU read it in the last timed step (appended token
+        # included): the CPU baseline runs on these same bytes
+        res_sample = dict(k=cache.key[0].cpu(), v=cache.value[0].cpu(), q=q[0].cpu(),
+                          tables=tables.clone())
     res = dict(us_per_layer=avg_s * 1e6, median_us_per_layer=statistics.median(decode_ms) * 1e3,
                ms_per_step=total_ms / steps, alg_bytes=alg_bytes,
                achieved_gbps=alg_bytes / avg_s / 1e9, split="balanced",
                fixed512_us_per_layer=fixed_s * 1e6,
                fixed512_GBps=alg_bytes / fixed_s / 1e9,
                read_ceiling_GBps=read_ceiling, pattern_ceiling_GBps=pattern_ceiling)
+    if keep_cpu_sample:
+        res["cpu_sample"] = res_sample
     del cache, q, k_new, v_new, out, ws
     torch.cuda.empty_cache()
     return res
 
 
-def bench_cpu_baseline(torch) -> dict:
-    """The reference CPU torch path for config 3 on a bounded sample: one layer, 2 of the
-    16 sequences (2 x 32768 context), gather + repeat_interleave + SDPA in bf16; the
-    per-layer time is scaled by 16/2 to the full batch."""
+def bench_cpu_baseline(torch, sample) -> dict:
+    """The reference's CPU torch path for config 3 (per-sequence gather + repeat_interleave
+    + SDPA, ref_torch.decode_repeat_kv_sdpa, in bf16) on one whole layer of the GPU run:
+    the same 16 x 32768 block tables, q and K/V bytes the GPU decoded in its last timed
+    step, on every host core this process may use.  One warmup, then the median of 5."""
     from oracle import ref_torch
 
     c = C3
-    Hq, KVH, D, bs, ctx = c["hq"], c["kvh"], c["d"], c["bs"], c["ctx"]
-    nseq, B = 2, c["batch"]
-    torch.set_num_threads(len(os.sched_getaffinity(0)))
-    nb = nseq * ctx // bs
-    g = torch.Generator().manual_seed(3101)
-    kc = torch.randn((nb * bs, KVH, D), generator=g).to(torch.bfloat16)
-    vc = torch.randn((nb * bs, KVH, D), generator=g).to(torch.bfloat16)
-    perm = torch.randperm(nb, generator=g)
-    slot_lists = [(perm[i * (ctx // bs):(i + 1) * (ctx // bs)][:, None] * bs
-                   + torch.arange(bs)[None]).reshape(-1) for i in range(nseq)]
-    q = torch.randn((nseq, Hq, D), generator=g).to(torch.bfloat16)
+    Hq, KVH, bs, ctx, B = c["hq"], c["kvh"], c["bs"], c["ctx"], c["batch"]
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    kc, vc, q, tables = sample["k"], sample["v"], sample["q"], sample["tables"]
+    slot_lists = [(tables[b].long()[:, None] * bs + torch.arange(bs)[None]).reshape(-1)[:ctx]
+                  for b in range(B)]
     times = []
-    for _ in range(3):
+    for _ in range(6):
         t = time.perf_counter()
         ref_torch.decode_repeat_kv_sdpa(q, kc, vc, slot_lists, Hq // KVH)
         times.append(time.perf_counter() - t)
-    per_layer = statistics.median(times[1:]) * (B / nseq)
-    return dict(value=round(per_layer * 1e6, 1), unit="us/layer",
-                cores=torch.get_num_threads(), kind="port",
-                sample=f"config 3, 1 layer, {nseq} of {B} sequences x {ctx} tokens, median of "
-                       f"{len(times) - 1} after 1 warmup, scaled x{B // nseq}",
+    per_layer = statistics.median(times[1:])
+    return dict(value=round(per_layer * 1e6, 1), unit="us/layer", cores=cores,
+                torch_threads=torch.get_num_threads(), kind="port",
+                sample=f"config 3, one whole layer ({B} x {ctx} tokens, the GPU run's own "
+                       f"layer-0 tensors), median of 5 after 1 warmup",
                 cpu_model=_cpu_model(), transport=_xfer_reference(torch))
 
 
@@ -242,6 +299,15 @@ def _xfer_reference(torch) -> dict:
 
 
 def _cpu_model() -> str:
+    """`lscpu`'s model name (the /proc/cpuinfo line if lscpu is missing)."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            if line.strip().startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
@@ -547,7 +613,8 @@ def bench_c4(torch) -> dict:
         pairs += p
     src = torch.tensor([p[0] for p in pairs], dtype=torch.int32, device=dev)
     dst = torch.tensor([p[1] for p in pairs], dtype=torch.int32, device=dev)
-    cow_s = _time_gpu(torch, lambda: cache.copy_blocks_device(cache, src, dst), 20)
+    cow_s = _time_gpu_cold(torch, lambda: cache.copy_blocks_device(cache, src, dst), 20)
+    cow_warm_s = _time_gpu(torch, lambda: cache.copy_blocks_device(cache, src, dst), 20)
     cow_bytes = 2 * 2 * L * len(pairs) * cache.block_bytes
     # suffix + draft tokens: one append per layer for all 32 sequences
     rows, wslots = [], []
@@ -559,7 +626,8 @@ def bench_c4(torch) -> dict:
     wslots_t = torch.tensor(wslots, device=dev)
     n = len(wslots)
     kr = torch.randn((n, KVH, D), generator=g, device=dev).to(torch.bfloat16)
-    app_s = _time_gpu(torch, lambda: cache.write(3, wslots_t, kr, kr), 20)
+    app_s = _time_gpu_cold(torch, lambda: cache.write(3, wslots_t, kr, kr), 20)
+    app_warm_s = _time_gpu(torch, lambda: cache.write(3, wslots_t, kr, kr), 20)
     # 5-query verify over ctx = prefix + suffix + 5
     ctx = [prefix + suffix[s] + K for s in range(S)]
     bt = cache.block_table([mgr.block_table(s).block_ids for s in range(S)])
@@ -613,12 +681,15 @@ def bench_c4(torch) -> dict:
     spill = PagedKVCache(L, nev, bs, KVH, D, device=dev)
     esrc = torch.tensor(live[:nev], dtype=torch.int32, device=dev)
     edst = torch.arange(nev, dtype=torch.int32, device=dev)
-    ev_s = _time_gpu(torch, lambda: spill.copy_blocks_device(cache, esrc, edst), 20)
+    ev_s = _time_gpu_cold(torch, lambda: spill.copy_blocks_device(cache, esrc, edst), 20)
+    ev_warm_s = _time_gpu(torch, lambda: spill.copy_blocks_device(cache, esrc, edst), 20)
     cache.check_errors()
     spill.check_errors()
     res = {
         "c4_cow_pairs": len(pairs), "c4_cow_us": cow_s * 1e6, "c4_cow_GBps": cow_bytes / cow_s / 1e9,
+        "c4_cow_warm_GBps": cow_bytes / cow_warm_s / 1e9,
         "c4_append_rows": n, "c4_append_GBps": 2 * 2 * n * cache.row_bytes / app_s / 1e9,
+        "c4_append_warm_GBps": 2 * 2 * n * cache.row_bytes / app_warm_s / 1e9,
         "c4_verify_us_per_layer": ver_s * 1e6,
         "c4_verify_shared_prefix_tokens": shared_tokens,
         "c4_verify_plain_us_per_layer": plain_s * 1e6,
@@ -629,6 +700,7 @@ def bench_c4(torch) -> dict:
         "c4_fork_decode_plain_us_per_layer": dec_plain_s * 1e6,
         "c4_evict_blocks": nev, "c4_evict_us": ev_s * 1e6,
         "c4_evict_GBps": 2 * 2 * L * nev * cache.block_bytes / ev_s / 1e9,
+        "c4_evict_warm_GBps": 2 * 2 * L * nev * cache.block_bytes / ev_warm_s / 1e9,
     }
     del cache, spill
     torch.cuda.empty_cache()
@@ -776,7 +848,7 @@ def bench_c5(torch) -> dict:
     cu = torch.arange(0, (R + 1) * T, T, dtype=torch.int64, device=dev)
     kbuf = torch.empty((Ls * R * T, KVH, D), dtype=torch.bfloat16, device=dev)
     vbuf = torch.empty_like(kbuf)
-    g_s = _time_gpu(torch, lambda: src.gather_into(bt, cu, T, kbuf, vbuf), 10)
+    g_s = _time_gpu_cold(torch, lambda: src.gather_into(bt, cu, T, kbuf, vbuf), 10)
     src.check_errors()
     moved = 2 * 2 * Ls * R * T * src.row_bytes
     del src
@@ -808,19 +880,21 @@ def bench_c5(torch) -> dict:
     tgt = PagedKVCache(Lt, NB, bs, KVH, D, device=dev)
     perm = torch.randperm(NB, generator=gcpu)[:nb].view(R, T // bs)
     bt2 = perm.to(torch.int32).to(dev)
-    s_s = _time_gpu(torch, lambda: tgt.scatter_from(bt2, cu, T, mk, mv), 10)
+    s_s = _time_gpu_cold(torch, lambda: tgt.scatter_from(bt2, cu, T, mk, mv), 10)
     tgt.check_errors()
     # prefill-scale append of 32768 rows (2 KiB) into random slots of one layer
     n = 32768
     slots = torch.randperm(tgt.num_slots, generator=gcpu)[:n].to(dev)
     kr, vr = mk[:n], mv[:n]
-    a_s = _time_gpu(torch, lambda: tgt.write(3, slots, kr, vr), 20)
+    a_s = _time_gpu_cold(torch, lambda: tgt.write(3, slots, kr, vr), 20)
+    a_warm_s = _time_gpu(torch, lambda: tgt.write(3, slots, kr, vr), 20)
     res = {"c5_gather_us": g_s * 1e6, "c5_gather_GBps": moved / g_s / 1e9,
            "c5_map_ms": m_s * 1e3, "c5_map_TFLOPs": flops / m_s / 1e12,
            "c5_map_mfma_frac": flops / m_s / 1e12 / PEAK_BF16_TFLOPS,
            "c5_scatter_us": s_s * 1e6,
            "c5_scatter_GBps": 2 * 2 * Lt * R * T * tgt.row_bytes / s_s / 1e9,
-           "append_prefill_GBps": 2 * 2 * n * tgt.row_bytes / a_s / 1e9}
+           "append_prefill_GBps": 2 * 2 * n * tgt.row_bytes / a_s / 1e9,
+           "append_prefill_warm_GBps": 2 * 2 * n * tgt.row_bytes / a_warm_s / 1e9}
     del tgt, kbuf, vbuf, mk, mv
     torch.cuda.empty_cache()
     return res
@@ -843,7 +917,7 @@ def bench_copy_ceiling(torch) -> dict:
     64, 16 and 4 KiB per workgroup, the last two one-shot workgroups -- read + write bytes
     over time."""
     from dispec_amd import _lib
-    lib = _lib.lib()
+    lib = _probe_lib()
     n = 2 << 30
     src = torch.empty(n, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
@@ -911,13 +985,13 @@ def main() -> int:
         print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v)
                           for k, v in aux.items()}), flush=True)
         return 0
-    dec = bench_decode(torch, args.steps, args.warmup)
+    dec = bench_decode(torch, args.steps, args.warmup, keep_cpu_sample=not args.no_cpu_baseline)
     aux = {}
     if not args.no_aux:
         for name, fn in configs[:8]:
             _log(f"config {name}")
             aux.update(fn(torch))
-    cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch)
+    cpu = None if args.no_cpu_baseline else bench_cpu_baseline(torch, dec.pop("cpu_sample"))
     line = {
         "metric": "paged decode attn us/layer (Qwen3-4B shape, 16 x 32768 ctx)",
         "value": round(dec["us_per_layer"], 2),

@@ -66,10 +66,6 @@ SIGNATURES: dict[str, tuple] = {
                                         c_int64, _P, _P, c_float, _P, _P, c_int64, _P, c_int64,
                                         c_int32, c_int32, c_int32, _P, c_int64, c_int64, _P, _P,
                                         c_int64, c_int64, c_int64, c_int32, _P, _P]),
-    "dsp_probe_stream_read": (c_int, [_P, c_int64, c_int32, _P, _P]),
-    "dsp_probe_stream_copy": (c_int, [_P, _P, c_int64, c_int32, _P]),
-    "dsp_probe_slice_read": (c_int, [_P, _P, c_int64, _P, c_int64, c_int32, c_int32, c_int32,
-                                     c_int32, c_int32, _P, _P]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -1,8 +1,9 @@
 """Build libdispec_hip.so from dispec_amd/csrc/*.hip for gfx950 with hipcc.
 
 Every source is compiled to an object in dispec_amd/_build/ (in parallel), then linked
-into dispec_amd/libdispec_hip.so in-tree, where the loader looks for it.  Run as
-`python -m dispec_amd.build`.
+into dispec_amd/libdispec_hip.so in-tree, where the loader looks for it.  The bandwidth
+probes of dispec_amd/probe/ go into a separate libdispec_probe.so that only bench.py
+loads.  Run as `python -m dispec_amd.build`.
 """
 
 from __future__ import annotations
@@ -18,6 +19,9 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ_DIR = PKG / "_build"
 LIB = PKG / "libdispec_hip.so"
+# measurement-only kernels (bench.py's bandwidth probes), kept out of the product library
+PROBE_SRC = PKG / "probe"
+PROBE_LIB = PKG / "libdispec_probe.so"
 ARCH = os.environ.get("DISPEC_HIP_ARCH", "gfx950")
 
 # Packed-fp32 VALU ops are switched off for all device code: hipcc would otherwise form
@@ -48,25 +52,33 @@ def _compile(src: Path, verbose: bool) -> Path:
     return obj
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every csrc/*.hip and link libdispec_hip.so. Returns the library path."""
-    sources = sorted(CSRC.glob("*.hip"))
-    if not sources:
-        raise RuntimeError(f"no HIP sources under {CSRC}")
-    OBJ_DIR.mkdir(exist_ok=True)
-    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2)))
-    with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(s, verbose), sources))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs: list[Path], lib: Path, verbose: bool) -> Path:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
            *map(str, objs)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
-    return LIB
+        raise RuntimeError(f"link of {lib.name} failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, lib)
+    return lib
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every csrc/*.hip into libdispec_hip.so (the product library) and every
+    probe/*.hip into libdispec_probe.so (bench-side).  Returns the product library path."""
+    sources = sorted(CSRC.glob("*.hip"))
+    probes = sorted(PROBE_SRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    OBJ_DIR.mkdir(exist_ok=True)
+    jobs = jobs or min(len(sources) + len(probes), max(1, (os.cpu_count() or 2)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda s: _compile(s, verbose), sources + probes))
+    if probes:
+        _link(objs[len(sources):], PROBE_LIB, verbose)
+    return _link(objs[:len(sources)], LIB, verbose)
 
 
 if __name__ == "__main__":

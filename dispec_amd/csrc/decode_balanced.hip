@@ -345,9 +345,9 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
       // This chunk's V has landed once at most the next chunk's K loads (2 * NKK) and a
       // window load remain outstanding; loads complete in issue order.
       if (prefetch)
-        __builtin_amdgcn_s_waitcnt(((2 * NKK) & 15) | 0x0F70);
+        __builtin_amdgcn_s_waitcnt(dsp_waitcnt_vm<2 * NKK>());
       else
-        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_waitcnt(dsp_waitcnt_vm<0>());
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

@@ -38,6 +38,20 @@ static inline int dsp_vec_width(std::initializer_list<int64_t> vals) {
   return w;
 }
 
+// s_waitcnt immediate that waits until at most VM vector-memory operations of this wave
+// are outstanding and does not wait on the export or LDS/scalar counters.  gfx9
+// encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4] (7 = no wait), lgkmcnt [11:8]
+// (15 = no wait).  The vmcnt field holds 0..63: a count beyond it is a compile error, not
+// a silently wrapped wait.
+template <int VM>
+constexpr int dsp_waitcnt_vm() {
+  static_assert(VM >= 0 && VM <= 63, "vmcnt holds 0..63 outstanding loads on gfx9");
+  return (VM & 15) | ((VM >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+static_assert(dsp_waitcnt_vm<0>() == 0x0F70 && dsp_waitcnt_vm<8>() == 0x0F78 &&
+                  dsp_waitcnt_vm<17>() == 0x4F71,
+              "s_waitcnt encoding");
+
 // ---------------------------------------------------------------- device helpers
 // Byte vectors used for coalesced copies.  16 B per lane is one global_load_dwordx4.
 // Native clang vectors, not HIP's uint4/uint2 structs: conditional loads of the struct

@@ -226,9 +226,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     // This chunk's V has landed in the slab: every VMEM op issued after it is the next
     // chunk's K (2 * NKK loads, when prefetching).
     if (prefetch)
-      __builtin_amdgcn_s_waitcnt(((2 * NKK) & 15) | 0x0F70);
+      __builtin_amdgcn_s_waitcnt(dsp_waitcnt_vm<2 * NKK>());
     else
-      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __builtin_amdgcn_s_waitcnt(dsp_waitcnt_vm<0>());
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

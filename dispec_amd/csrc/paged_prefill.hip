@@ -253,7 +253,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     // barrier every wave's are, and every wave is done reading chunk c - 1, whose buffer
     // the next DMA overwrites
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __builtin_amdgcn_s_waitcnt(dsp_waitcnt_vm<0>());
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
     if (c + 1 < nch) {

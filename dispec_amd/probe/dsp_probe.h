@@ -1,0 +1,44 @@
+/*
+ * dsp_probe.h -- measurement-only kernels of libdispec_probe.so (not part of the C ABI of
+ * libdispec_hip.so; nothing in the KV path calls them).  bench.py uses them to calibrate
+ * what this GPU's HBM delivers to the access patterns of the path's kernels.
+ */
+#ifndef DISPEC_PROBE_H
+#define DISPEC_PROBE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#include "../../include/dispec_hip.h" /* dsp_stream_t, DSP_E* */
+
+/* Probes with no counterpart in the reference.  Each returns 0, a negative DSP_E* status
+ * of dispec_hip.h for an invalid argument (nothing launched), or a positive hipError_t.
+ *   dsp_probe_stream_read: `workgroups` workgroups stream `bytes` of `buf` (16-byte
+ *     aligned) once.
+ *   dsp_probe_slice_read: the paged decode's access pattern without its arithmetic --
+ *     for each (sequence, KV head) `waves_per_seq_head` waves read that head's 128-dim
+ *     bf16 row of K and V for all `ctx` keys through `block_table`, the waves of 4 heads
+ *     of the same keys side by side in one workgroup when KVH % 4 == 0 (as the balanced
+ *     decode kernel groups them); caches are [num_slots, KVH, 128] contiguous; ctx a
+ *     multiple of 32 * waves_per_seq_head.
+ * Both store one word to `sink` only if what they read hashes to a sentinel. */
+int dsp_probe_stream_read(const void* buf, int64_t bytes, int32_t workgroups, uint32_t* sink,
+                          dsp_stream_t stream);
+/*   dsp_probe_stream_copy: `workgroups` workgroups copy `bytes` from src to dst (both
+ *     16-byte aligned, not overlapping) once: the ceiling of the byte-moving kernels. */
+int dsp_probe_stream_copy(const void* src, void* dst, int64_t bytes, int32_t workgroups,
+                          dsp_stream_t stream);
+int dsp_probe_slice_read(const void* k_cache, const void* v_cache, int64_t num_slots,
+                         const int32_t* block_table, int64_t bt_stride, int32_t block_size,
+                         int32_t B, int32_t KVH, int32_t ctx, int32_t waves_per_seq_head,
+                         uint32_t* sink, dsp_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DISPEC_PROBE_H */
