@@ -20,6 +20,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libdispec_hip.so"
 
 DSP_BF16, DSP_F16, DSP_F32 = 0, 1, 2
 DSP_OK, DSP_EINVAL, DSP_EALIGN, DSP_EUNSUPPORTED, DSP_EWORKSPACE = 0, -1, -2, -3, -4
+DSP_ESCRATCH = -5
+DSP_NOALLOC_SCRATCH_BYTES = 32 << 20   # fixed workspace of dsp_paged_decode_noalloc
 DSP_SPLIT_BALANCED = -1   # partition_tokens of dsp_paged_mq_attention: balanced split-K
 
 # (name, restype, argtypes) for every symbol the header declares.
@@ -45,6 +47,10 @@ SIGNATURES: dict[str, tuple] = {
                                  _P, c_int64, c_int32, _P, c_int64, _P, c_int32, c_int32,
                                  c_int32, c_int32, c_float, c_int32, c_int32, _P, c_size_t,
                                  _P, c_int64, c_int64, c_int32, _P, _P]),
+    "dsp_paged_decode_noalloc": (c_int, [_P, c_int64, c_int64, _P, _P, c_int64, c_int64,
+                                         c_int64, _P, c_int64, c_int32, _P, c_int64, _P,
+                                         c_int32, c_int32, c_int32, c_int32, c_float, c_int32,
+                                         c_int32, _P, c_int64, c_int64, c_int32, _P, _P]),
     "dsp_paged_mq_partition_tokens": (c_int, [c_int32] * 6),
     "dsp_paged_mq_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32,
                                                 c_int32, c_int32]),

@@ -8,6 +8,9 @@ extern "C" const char* dsp_error_string(int status) {
     case DSP_EALIGN: return "misaligned pointer or stride for the vectorised kernel";
     case DSP_EUNSUPPORTED: return "dtype, head_dim or query-group size has no compiled kernel";
     case DSP_EWORKSPACE: return "workspace smaller than the size the launch needs";
+    case DSP_ESCRATCH:
+      return "the launch needs more split-K workspace than the no-allocation entry point's "
+             "fixed scratch (DSP_NOALLOC_SCRATCH_BYTES)";
     default:
       if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));
       return "unknown dispec_hip status";

@@ -26,6 +26,8 @@
 // for GQA groups of 6+); this VALU kernel serves per-token slot tables and head_dim 16.
 #include <float.h>
 
+#include <mutex>
+
 #include "dsp_common.h"
 #include "dsp_internal.h"
 
@@ -568,4 +570,62 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
     launch_combine<F16Tag>(D, cgrid, s, ws_acc, ws_ml, ctx_lens, max_ctx, P, num_parts, Hq, oh,
                            o_stride_b, o_stride_h);
   return dsp_launch_status();
+}
+
+// ------------------------------------------------------------------ no-allocation variant
+// dsp_paged_decode with its split-K workspace in a file-scope device array instead of a
+// caller buffer, for callers that cannot allocate (graph capture, serving loops).  In host
+// code `scratch` names a host-side stand-in, not device memory: its device address is
+// fetched once per device with hipGetSymbolAddress (with that device current) and only
+// that address is ever passed to a kernel.  The decode kernels write every workspace word
+// they later read, so nothing has to be cleared between calls.
+namespace {
+
+__device__ __align__(256) unsigned char scratch[DSP_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::once_flag g_scratch_once[kMaxScratchDevices];
+void* g_scratch_ptr[kMaxScratchDevices];
+int g_scratch_status[kMaxScratchDevices];
+
+// The current device's copy of `scratch` (status 0), set up on the first call per device.
+int scratch_for_current_device(void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxScratchDevices) return DSP_EUNSUPPORTED;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_status[dev] = r == hipSuccess ? (p ? DSP_OK : DSP_EINVAL) : static_cast<int>(r);
+    g_scratch_ptr[dev] = p;
+  });
+  *ptr = g_scratch_ptr[dev];
+  return g_scratch_status[dev];
+}
+
+}  // namespace
+
+extern "C" int dsp_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                        const void* k_cache, const void* v_cache,
+                                        int64_t num_slots, int64_t kv_stride_slot,
+                                        int64_t kv_stride_head, const int32_t* block_table,
+                                        int64_t bt_stride, int32_t block_size,
+                                        const int32_t* slot_table, int64_t st_stride,
+                                        const int32_t* ctx_lens, int32_t B, int32_t Hq,
+                                        int32_t KVH, int32_t D, float scale, int32_t max_ctx,
+                                        int32_t partition_tokens, void* out, int64_t o_stride_b,
+                                        int64_t o_stride_h, int32_t dtype, int32_t* err_count,
+                                        dsp_stream_t stream) {
+  // the launch's workspace must fit the fixed scratch; checked before any device work
+  const size_t need = dsp_paged_decode_workspace_bytes(B, Hq, KVH, D, max_ctx, partition_tokens);
+  DSP_HOST_CHECK(need <= DSP_NOALLOC_SCRATCH_BYTES, DSP_ESCRATCH);
+  void* ws = nullptr;
+  const int st = scratch_for_current_device(&ws);
+  if (st != DSP_OK) return st;
+  return dsp_paged_decode(q, q_stride_b, q_stride_h, k_cache, v_cache, num_slots,
+                          kv_stride_slot, kv_stride_head, block_table, bt_stride, block_size,
+                          slot_table, st_stride, ctx_lens, B, Hq, KVH, D, scale, max_ctx,
+                          partition_tokens, ws, DSP_NOALLOC_SCRATCH_BYTES, out, o_stride_b,
+                          o_stride_h, dtype, err_count, stream);
 }

@@ -42,7 +42,8 @@ enum dsp_status {
   DSP_EINVAL = -1,        /* null pointer, negative size, inconsistent shape */
   DSP_EALIGN = -2,        /* a stride or pointer breaks the alignment a kernel needs */
   DSP_EUNSUPPORTED = -3,  /* dtype / head_dim / group size with no compiled kernel */
-  DSP_EWORKSPACE = -4     /* workspace smaller than dsp_*_workspace_bytes() */
+  DSP_EWORKSPACE = -4,    /* workspace smaller than dsp_*_workspace_bytes() */
+  DSP_ESCRATCH = -5       /* a no-allocation call needs more than its fixed scratch */
 };
 
 /* partition_tokens value of dsp_paged_mq_attention (and its workspace size) that asks for
@@ -172,6 +173,29 @@ int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                      void* workspace, size_t workspace_bytes,
                      void* out, int64_t o_stride_b, int64_t o_stride_h,
                      int32_t dtype, int32_t* err_count, dsp_stream_t stream);
+
+/* J3 without a workspace argument.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The same arguments and results as dsp_paged_decode
+ * (same kernels and split), with the split-K workspace taken from a fixed device array of
+ * DSP_NOALLOC_SCRATCH_BYTES held by the library on each GPU it runs on until the process
+ * ends; the call itself allocates nothing.  A launch whose workspace
+ * (dsp_paged_decode_workspace_bytes) exceeds it returns DSP_ESCRATCH with nothing
+ * launched (config 3's 16 x 32k batch needs 6.7 MB on the automatic split, 17 MB on
+ * 512-token partitions).  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be ordered by the
+ * caller.  The array's device address is fetched on the first call on each device (with
+ * that device current). */
+#define DSP_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int dsp_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void* k_cache, const void* v_cache, int64_t num_slots,
+                             int64_t kv_stride_slot, int64_t kv_stride_head,
+                             const int32_t* block_table, int64_t bt_stride, int32_t block_size,
+                             const int32_t* slot_table, int64_t st_stride,
+                             const int32_t* ctx_lens, int32_t B, int32_t Hq, int32_t KVH,
+                             int32_t D, float scale, int32_t max_ctx, int32_t partition_tokens,
+                             void* out, int64_t o_stride_b, int64_t o_stride_h, int32_t dtype,
+                             int32_t* err_count, dsp_stream_t stream);
 
 /* ------------------------------------------------------------------------------ J4
  * Multi-query paged attention for speculative verify and chunked prefill.
