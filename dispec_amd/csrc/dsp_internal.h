@@ -62,13 +62,13 @@ int prefill_attention(const uint16_t* q, int64_t q_stride_t, int64_t q_stride_h,
 // dsp_paged_mq_attention_shared_prefix in one launch: prefix tiles (every query row of the
 // batch, token-major via cu_q, against the first prefix_tokens keys of block-table row 0,
 // in prefix_tokens / P partitions) beside suffix tiles (each sequence's rows over its keys
-// from prefix_tokens on, causal, as partition prefix_tokens / P); partial results in the
-// merge layout with prefix_tokens / P + 1 partitions per 16-row tile.  A sequence with
+// from prefix_tokens on, causal, in partitions of P numbered on from the prefix's); partial
+// results in the merge layout, ceil(max_ctx / P) partitions per 16-row tile.  A sequence with
 // bad lengths or ctx - q_len < prefix_tokens is counted and zeroed.  `applies` says
 // whether the shape is served; `grid` is the launch's workgroups per KV head.
 bool shared_prefix_applies(int32_t D, int32_t block_size, int32_t B, int64_t num_slots,
                            int64_t kv_stride_slot);
-int64_t shared_prefix_grid(int32_t B, int32_t G, int32_t max_q_len, int32_t P,
+int64_t shared_prefix_grid(int32_t B, int32_t G, int32_t max_q_len, int32_t max_ctx, int32_t P,
                            int32_t prefix_tokens);
 int prefill_shared_prefix(const uint16_t* q, int64_t q_stride_t, int64_t q_stride_h,
                           const uint16_t* k_cache, const uint16_t* v_cache, int64_t num_slots,

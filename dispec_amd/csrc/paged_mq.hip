@@ -306,21 +306,39 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
 }
 
 // Merge the key partitions of one (tile, KV head, sequence).  Grid = (tiles * 16 / R, KVH,
-// B) with R = 256 / D rows per workgroup: one thread per (row, dim) output.  Each row's
-// partition weights 2^(m_p - M) and 1 / L are reduced across the row's first lanes and
-// kept in LDS; the partial accumulators are then read 8 partitions at a time.
+// B) with R = 256 / D rows per workgroup: one thread per (row, dim) output.  Every thread
+// folds its row's partitions itself, 16 at a time with a running maximum, so the merge
+// waits on one memory round trip: the first 16 partitions' (max, sum) pairs and its
+// accumulator elements are loaded together with the sequence's lengths, before it is
+// known how many of them the row has (all lie inside the workspace; those past the row's
+// count, possibly never written, are discarded by a select, not weighted).
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void mq_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
     int32_t G, int32_t P, int32_t num_parts, int32_t tiles_max, int32_t prefix_tokens,
-    int32_t fixed_parts, uint16_t* __restrict__ out, int64_t ost, int64_t osh) {
-  constexpr int R = 256 / D;            // rows per workgroup
-  constexpr int W = D < 64 ? D : 64;    // lanes that reduce one row's partition weights
-  __shared__ float s_w[R][kMaxParts];
-  __shared__ float s_inv[R];
+    uint16_t* __restrict__ out, int64_t ost, int64_t osh) {
+  constexpr int R = 256 / D;   // rows per workgroup
+  constexpr int kBatch = 16;   // partitions in flight per thread
   const int tile = blockIdx.x / (16 / R), rsub = blockIdx.x % (16 / R);
   const int kvh = blockIdx.y, b = blockIdx.z, KVH = gridDim.y;
+  const int rl = threadIdx.x / D, d = threadIdx.x % D;
+  const int rr = rsub * R + rl;
+  const int64_t slot0 = ((int64_t(b) * KVH + kvh) * tiles_max + tile) * num_parts;
+  const float* src = ws_acc + (slot0 * 16 + rr) * D + d;
+  const float* mlp = ws_ml + 2 * (slot0 * 16 + rr);
+  constexpr int64_t kAccStride = int64_t(16) * D, kMlStride = 32;  // floats per partition
+  float va[kBatch], vm[kBatch], vl[kBatch];
+  auto load = [&](int p0, int n) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (u < n) {
+        va[u] = src[(p0 + u) * kAccStride];
+        vm[u] = mlp[(p0 + u) * kMlStride];
+        vl[u] = mlp[(p0 + u) * kMlStride + 1];
+      }
+  };
+  load(0, min(num_parts, kBatch));
   const int q0 = cu_q[b];
   const int qlen = cu_q[b + 1] - q0;
   const int ctx = ctx_lens[b];
@@ -330,46 +348,34 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
     return;
   const int r_last = min(r0 + 15, rows - 1);
   const int kend = ctx - qlen + r_last / G + 1;
-  // a shared-prefix launch writes fixed_parts partitions for every row
-  const int nparts = fixed_parts > 0 ? fixed_parts : (kend > 0 ? (kend + P - 1) / P : 1);
-  if (nparts <= 1) return;  // written directly by the attention kernel
-  const int64_t slot0 = ((int64_t(b) * KVH + kvh) * tiles_max + tile) * num_parts;
-  const int rl = threadIdx.x / D, d = threadIdx.x % D;
-  const int rr = rsub * R + rl;
-  {
-    float M = -INFINITY;
-    if (d < W)
-      for (int p = d; p < nparts; p += W) M = fmaxf(M, ws_ml[2 * ((slot0 + p) * 16 + rr)]);
-#pragma unroll
-    for (int mask = 1; mask < W; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
-    const float Mu = M == -INFINITY ? 0.f : M;
-    float L = 0.f;
-    if (d < W)
-      for (int p = d; p < nparts; p += W) {
-        const float w = dsp_exp2(ws_ml[2 * ((slot0 + p) * 16 + rr)] - Mu);
-        s_w[rl][p] = w;
-        L = fmaf(ws_ml[2 * ((slot0 + p) * 16 + rr) + 1], w, L);
-      }
-#pragma unroll
-    for (int mask = 1; mask < W; mask <<= 1) L += dsp_shfl_xor(L, mask);
-    if (d == 0) s_inv[rl] = L > 0.f ? 1.f / L : 0.f;
-  }
-  __syncthreads();
+  // partitions of P keys up to the tile's last visible key (a shared-prefix launch numbers
+  // its prefix and suffix partitions the same way)
+  const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
   const int row = r0 + rr;
-  if (row >= rows) return;
-  const float* src = ws_acc + (slot0 * 16 + rr) * D + d;
-  const int64_t pstride = int64_t(16) * D;
-  float A = 0.f;
-  for (int p0 = 0; p0 < nparts; p0 += 8) {
-    float v[8];
+  if (nparts <= 1 || row >= rows) return;  // nparts 1: written by the attention kernel
+  float M = -INFINITY, L = 0.f, A = 0.f;
+  for (int p0 = 0; p0 < nparts; p0 += kBatch) {
+    const int n = min(nparts - p0, kBatch);
+    if (p0 > 0) load(p0, n);
+    float bm = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = p0 + u < nparts ? src[(p0 + u) * pstride] : 0.f;
+    for (int u = 0; u < kBatch; ++u) bm = u < n ? fmaxf(bm, vm[u]) : bm;
+    const float Mn = fmaxf(M, bm);
+    const float Mu = Mn == -INFINITY ? 0.f : Mn;
+    const float keep = dsp_exp2(M - Mu);   // 0 while nothing has been folded (M = -inf)
+    L *= keep;
+    A *= keep;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
-      if (p0 + u < nparts) A = fmaf(v[u], s_w[rl][p0 + u], A);
+    for (int u = 0; u < kBatch; ++u) {
+      const float w = u < n ? dsp_exp2(vm[u] - Mu) : 0.f;
+      L = fmaf(u < n ? vl[u] : 0.f, w, L);
+      A = fmaf(u < n ? va[u] : 0.f, w, A);
+    }
+    M = Mn;
   }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
   const int qrow = q0 + row / G, hh = kvh * G + row % G;
-  out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(A * s_inv[rl]);
+  out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(A * inv);
 }
 
 template <typename Tag, bool kDecode = false, typename... A>
@@ -554,7 +560,6 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                    DSP_EUNSUPPORTED);
   }
   const int num_parts = max_ctx > 0 ? (max_ctx + P - 1) / P : 1;
-  const int first_part = prefix_tokens / P;
   DSP_HOST_CHECK(num_parts <= kMaxParts, DSP_EINVAL);
   DSP_HOST_CHECK(tiles * num_parts < (int64_t(1) << 31), DSP_EINVAL);
   const size_t need = fixed_mq_workspace_bytes(B, Hq, KVH, D, max_q_len, max_ctx, P);
@@ -569,11 +574,11 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
   const int32_t lbs = dsp_log2i(block_size);
   const int32_t tm = static_cast<int32_t>(tiles);
   int st = DSP_OK;
-  int ws_parts = num_parts, fixed_parts = 0;
+  const int ws_parts = num_parts;
   if (prefix_tokens > 0) {
-    // prefix and suffix tiles in one launch, then a merge of first_part + 1 partitions
-    ws_parts = fixed_parts = first_part + 1;
-    DSP_HOST_CHECK(dsp_detail::shared_prefix_grid(B, G, max_q_len, P, prefix_tokens) <
+    // prefix and suffix tiles in one launch (the suffixes in partitions of P keys too),
+    // then the merge of every row's partitions
+    DSP_HOST_CHECK(dsp_detail::shared_prefix_grid(B, G, max_q_len, max_ctx, P, prefix_tokens) <
                        (int64_t(1) << 31),
                    DSP_EINVAL);
     st = dsp_detail::prefill_shared_prefix(qh, q_stride_t, q_stride_h, kh, vh, num_slots,
@@ -607,10 +612,10 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
              static_cast<unsigned>(B));
   if (!f16)
     return launch_mq_combine<Bf16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
-                                      ws_parts, tm, prefix_tokens, fixed_parts, oh, o_stride_t,
+                                      ws_parts, tm, prefix_tokens, oh, o_stride_t,
                                       o_stride_h);
   return launch_mq_combine<F16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
-                                   ws_parts, tm, prefix_tokens, fixed_parts, oh, o_stride_t,
+                                   ws_parts, tm, prefix_tokens, oh, o_stride_t,
                                    o_stride_h);
 }
 
@@ -625,12 +630,15 @@ extern "C" int dsp_paged_mq_shared_prefix_partition_tokens(int32_t B, int32_t Hq
   if (B <= 0 || KVH <= 0 || Hq % KVH != 0 || max_q_len <= 0 || prefix_tokens <= 0 ||
       prefix_tokens % 128 != 0)
     return 128;
-  // The prefix pass runs B * max_q_len * G rows per KV head in 128-row tiles: split the
-  // prefix until it has a workgroup for every other CU, in partitions that divide it (more,
-  // shorter partitions cost more in fixed per-workgroup latency and merge traffic than
-  // they gain; config 4: 256-key partitions 38 us, 128-key 43 us).
+  // The prefix pass runs B * max_q_len * G rows per KV head in 128-row tiles; the suffixes
+  // are cut into partitions of the same length.  Split the prefix until it has a workgroup
+  // for every fourth CU, in partitions that divide it: longer partitions leave the prefix
+  // tiles on too few CUs, shorter ones multiply the suffix workgroups past one round of
+  // resident tiles and the merge traffic (config 4, 32 forks of a 2050-token prompt, per
+  // layer: 5-query verify 29.1 us at 256 keys, 27.8 at 512; decode step 24.2 at 256, 30.7
+  // at 128).
   const int64_t tiles = dsp_detail::prefill_tiles(int32_t(int64_t(B) * max_q_len), Hq / KVH);
-  const int64_t want = int64_t(dsp_detail::device_cus()) / 2;
+  const int64_t want = int64_t(dsp_detail::device_cus()) / 4;
   for (int p = 512; p > 128; p -= 128)
     if (prefix_tokens % p == 0 && tiles * KVH * (prefix_tokens / p) >= want) return p;
   return 128;

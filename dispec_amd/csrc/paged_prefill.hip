@@ -76,9 +76,10 @@ typedef __attribute__((address_space(3))) v4i16 lds_v4i16_t;
 // first prefix_tokens of block-table row 0, which every sequence shares and every query
 // sees whole (no mask); partition `part` covers keys [part*P, part*P + P) and is written,
 // for every row, to that row's own (sequence, 16-row tile) slot of the merge layout.  The
-// other workgroups are suffix tiles: one sequence's rows over its keys from prefix_tokens
-// on (causal), written as partition prefix_tokens / P.  Both kinds run side by side; the
-// merge then folds prefix_tokens / P + 1 partitions per row.
+// other workgroups are suffix tiles: one sequence's rows over one partition of P of its
+// keys from prefix_tokens on (causal), numbered on from the prefix's partitions (keys
+// [part*P, part*P + P) again).  Both kinds run side by side; the merge then folds every
+// partition up to a row's last visible key, as for an unshared launch.
 template <typename Tag, int D, bool kShared>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void paged_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t qst, int64_t qsh, const uint16_t* __restrict__ kc,
@@ -119,16 +120,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       part = xl % num_parts;
       tile = prefix_x / num_parts - 1 - xl / num_parts;
     } else {
-      const int tiles_s = (X - prefix_x) / nseq, idx = xl - prefix_x;
-      b = idx / tiles_s;
-      tile = tiles_s - 1 - idx % tiles_s;
-      part = prefix_tokens / P;
+      // suffix tiles: per sequence tiles_s row tiles x nsp partitions of its keys past the
+      // prefix (partition index continues the prefix's: key range [part*P, part*P + P))
+      const int first = prefix_tokens / P, nsp = ws_parts - first;
+      const int per_seq = (X - prefix_x) / nseq, idx = xl - prefix_x;
+      const int tiles_s = per_seq / nsp, k = idx % per_seq;
+      b = idx / per_seq;
+      tile = tiles_s - 1 - k / nsp;
+      part = first + k % nsp;
     }
   } else {
     const int ntiles = X / num_parts;
     part = xl % num_parts;
     tile = ntiles - 1 - xl / num_parts;
   }
+  // The first two chunks' block ids are loaded now, beside the lengths below: chunk keys
+  // start at part * P whatever the lengths are (clamped into the table's width here; a
+  // wave whose rows turn out to start past the partition's end reloads its id below).
+  const int wave_e = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t bt_row_e = int64_t(b) * bt_stride;
+  const int key_cap = max(max_ctx - 1, 0);
+  auto early_blk = [&](int t) {
+    return bt[bt_row_e + (min(t + 16 * wave_e, key_cap) >> log2_bs)];
+  };
+  int32_t blk_first = early_blk(part * P), blk_second = early_blk(part * P + kChunk);
   int q0, qlen, ctx, kend = 0;
   if (pre) {
     // all tokens of the batch; the causal limit never binds (ctx - qlen + qi >= max_ctx)
@@ -163,11 +178,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     const int r_last = min(r0 + kRows - 1, rows - 1);
     kend = ctx - qlen + r_last / G + 1;  // keys any row of the tile sees
   }
-  // a suffix tile covers everything past the prefix in one partition
-  const bool suffix = kShared && !pre;
-  const int kbeg = suffix ? prefix_tokens : part * P;
+  // partition `part` covers keys [part*P, part*P + P) of the tile's visible range (a
+  // suffix tile's partitions start at the prefix's end, which is a multiple of P)
+  const int kbeg = part * P;
   if (kbeg >= kend) return;
-  const int kfin = suffix ? kend : min(kbeg + P, kend);
+  const int kfin = min(kbeg + P, kend);
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -175,6 +190,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   const int col = lane & 31;       // this lane's row within the wave
   const int r = r0 + 32 * wave + col;
   const bool row_ok = r < rows;
+  const bool wave_has_rows = r0 + 32 * wave < rows;  // wave-uniform
   const int qi = row_ok ? r / G : 0;
   const int h = kvh * G + (row_ok ? r % G : 0);
   // Keys 0..lim are visible to this row (causal limit, and the partition's end); lim_min
@@ -243,10 +259,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
     for (int j = 0; j < 16; ++j) acc[dt][j] = 0.f;
 
   const int nch = (kfin - kbeg + kChunk - 1) / kChunk;
-  // block ids run one chunk ahead of the DMAs, which run one chunk ahead of the MFMAs
-  int32_t blk = load_blk(kbeg);
-  issue(0, kbeg, blk);
-  if (nch > 1) blk = load_blk(kbeg + kChunk);
+  // block ids run one chunk ahead of the DMAs, which run one chunk ahead of the MFMAs; the
+  // first two were loaded at entry for the unclamped keys, which load_blk would clamp to
+  // kfin - 1 only for a wave whose rows start past kfin (then reloaded, as load_blk does)
+  if (kbeg + 16 * wave > kfin - 1) blk_first = load_blk(kbeg);
+  issue(0, kbeg, blk_first);
+  int32_t blk = blk_second;
+  if (nch > 1 && kbeg + kChunk + 16 * wave > kfin - 1) blk = load_blk(kbeg + kChunk);
   for (int c = 0; c < nch; ++c) {
     const int t0 = kbeg + c * kChunk;
     // this wave's DMAs of chunk c (and the block ids of chunk c + 1) are in; after the
@@ -260,6 +279,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       issue((c + 1) & 1, t0 + kChunk, blk);
       if (c + 2 < nch) blk = load_blk(t0 + 2 * kChunk);
     }
+    // A wave whose 32 rows all lie past the tile's rows (a short query block: a verify
+    // tile of 10 rows leaves three of four waves empty) only loads its share of each chunk.
+    if (!wave_has_rows) continue;
     const char* ks_lds = &lds[c & 1][0][0];
     const char* vs_lds = &lds[c & 1][1][0];
 
@@ -447,22 +469,24 @@ int prefill_shared_prefix(const uint16_t* q, int64_t q_stride_t, int64_t q_strid
                           int64_t o_stride_t, int64_t o_stride_h, bool f16, int32_t* err_count,
                           hipStream_t s) {
   const int32_t prefix_parts = prefix_tokens / P;
+  const int32_t suffix_parts = (max_ctx - prefix_tokens + P - 1) / P;
   const int64_t tiles_p = (int64_t(B) * max_q_len * G + kRows - 1) / kRows;
   const int64_t prefix_x = tiles_p * prefix_parts;
-  const int64_t suffix_x = int64_t(B) * prefill_tiles(max_q_len, G);
+  const int64_t suffix_x = int64_t(B) * prefill_tiles(max_q_len, G) * suffix_parts;
   dim3 grid(static_cast<unsigned>(prefix_x + suffix_x), static_cast<unsigned>(KVH), 1u);
   return launch_prefill<true>(D, f16, grid, s, q, q_stride_t, q_stride_h, k_cache, v_cache,
                               num_slots, kv_stride_slot, kv_stride_head, block_table, bt_stride,
                               log2_bs, cu_q, ctx_lens, max_ctx, G, scale_log2, P, prefix_parts,
                               tiles16_max, ws_acc, ws_ml, out, o_stride_t, o_stride_h, err_count,
-                              B, prefix_tokens, prefix_parts + 1,
+                              B, prefix_tokens, prefix_parts + suffix_parts,
                               static_cast<int32_t>(prefix_x));
 }
 
-int64_t shared_prefix_grid(int32_t B, int32_t G, int32_t max_q_len, int32_t P,
+int64_t shared_prefix_grid(int32_t B, int32_t G, int32_t max_q_len, int32_t max_ctx, int32_t P,
                            int32_t prefix_tokens) {
   const int64_t tiles_p = (int64_t(B) * max_q_len * G + kRows - 1) / kRows;
-  return tiles_p * (prefix_tokens / P) + int64_t(B) * prefill_tiles(max_q_len, G);
+  return tiles_p * (prefix_tokens / P) +
+         int64_t(B) * prefill_tiles(max_q_len, G) * ((max_ctx - prefix_tokens + P - 1) / P);
 }
 
 bool shared_prefix_applies(int32_t D, int32_t block_size, int32_t B, int64_t num_slots,
