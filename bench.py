@@ -882,6 +882,18 @@ def bench_c5(torch) -> dict:
     bt2 = perm.to(torch.int32).to(dev)
     s_s = _time_gpu_cold(torch, lambda: tgt.scatter_from(bt2, cu, T, mk, mv), 10)
     tgt.check_errors()
+
+    # the map with the scatter fused into its epilogue: each (target layer, K|V) GEMM
+    # writes its rows straight into the target pool's blocks (no 4.8 GB intermediate)
+    def run_map_fused():
+        for buf, pool in ((kbuf, tgt.key), (vbuf, tgt.value)):
+            for i, m in enumerate(maps):
+                assert m.apply_to_pool(buf, [m.source_layers[0] * T * kv], kv, kv, T, pool[i],
+                                       bt2, bs, None, batch=R, a_batch_stride=Ls * T * kv,
+                                       err=tgt._err)
+
+    mf_s = _time_gpu(torch, run_map_fused, 3, warmup=1)
+    tgt.check_errors()
     # prefill-scale append of 32768 rows (2 KiB) into random slots of one layer
     n = 32768
     slots = torch.randperm(tgt.num_slots, generator=gcpu)[:n].to(dev)
@@ -892,6 +904,10 @@ def bench_c5(torch) -> dict:
            "c5_map_ms": m_s * 1e3, "c5_map_TFLOPs": flops / m_s / 1e12,
            "c5_map_mfma_frac": flops / m_s / 1e12 / PEAK_BF16_TFLOPS,
            "c5_scatter_us": s_s * 1e6,
+           "c5_map_fused_scatter_ms": mf_s * 1e3,
+           "c5_map_fused_TFLOPs": flops / mf_s / 1e12,
+           "c5_pipeline_ms": (g_s + mf_s) * 1e3,
+           "c5_pipeline_unfused_ms": (g_s + m_s + s_s) * 1e3,
            "c5_scatter_GBps": 2 * 2 * Lt * R * T * tgt.row_bytes / s_s / 1e9,
            "append_prefill_GBps": 2 * 2 * n * tgt.row_bytes / a_s / 1e9,
            "append_prefill_warm_GBps": 2 * 2 * n * tgt.row_bytes / a_warm_s / 1e9}

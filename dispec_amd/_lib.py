@@ -66,6 +66,10 @@ SIGNATURES: dict[str, tuple] = {
     "dsp_kv_map_gemm": (c_int, [_P, _I64P, c_int32, c_int64, c_int64, _P, c_int64, _P, c_int64,
                                 c_int64, c_int64, c_int64, c_int32, c_int64, c_int64, _P, c_int32,
                                 c_int32, c_int32, c_int32, _P]),
+    "dsp_kv_map_gemm_to_pool": (c_int, [_P, _I64P, c_int32, c_int64, c_int64, _P, c_int64, _P,
+                                        c_int64, c_int64, _P, c_int64, c_int32, c_int64, c_int64,
+                                        c_int64, c_int32, c_int64, _P, _P, _P, c_int32, c_int32,
+                                        _P, _P]),
     "dsp_kv_rope": (c_int, [_P, c_int64, _P, c_int64, c_int64, c_int64, c_int64, c_int64, _P, _P,
                             c_int32, c_int32, c_int32, _P]),
     "dsp_qk_norm_rope_append": (c_int, [_P, c_int64, c_int64, _P, c_int64, c_int64, _P, c_int64,

@@ -255,14 +255,42 @@ static_assert(kBM * kCPR % (64 * kLPW) == 0, "a wave loads rows of one operand o
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
+// Where the rows of C go when they are scattered into a paged pool instead of a dense
+// matrix (kPool): row m of problem z is pool slot block_tables[z][m / bs] * bs + m % bs of
+// one layer, whose rows are ldc elements apart; a row whose block id lies outside the pool
+// is skipped and counted.  rope_cos / rope_sin (kRope): fp32 tables [M][head_dim], row m
+// the position of row m, applied after the bias (RoPE on each head of the row).
+struct PoolOut {
+  const int32_t* block_tables = nullptr;
+  int64_t bt_stride = 0;
+  int32_t log2_bs = 0;
+  int64_t num_slots = 0;
+  const float* rope_cos = nullptr;
+  const float* rope_sin = nullptr;
+  int32_t head_dim = 0;
+  int32_t* err_count = nullptr;
+};
+
+// out = x*cos + rotate_half(x)*sin for one element, x_partner the element half a head
+// away (rotate_half(x) = cat(-x2, x1)); the two products and the sum are each rounded to
+// fp32, the order of the reference's elementwise torch ops (transfer.py:76-80).
+__device__ __forceinline__ float rope_apply1(float x, float x_partner, float c, float sn,
+                                             bool first_half) {
+#pragma clang fp contract(off)
+  const float t1 = x * c;
+  const float t2 = x_partner * sn;
+  return first_half ? t1 - t2 : t1 + t2;
+}
+
 // The epilogue flags are template parameters: with all three variants compiled into one
-// body the epilogue's live ranges push the kernel past 256 VGPRs.
-template <int kBias, int kAct, int kAccum>
+// body the epilogue's live ranges push the kernel past 256 VGPRs.  kRope / kPool: the
+// fused target-RoPE and pool-scatter epilogue of dsp_kv_map_gemm_to_pool.
+template <int kBias, int kAct, int kAccum, int kRope = 0, int kPool = 0>
 __global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
     const uint16_t* __restrict__ a, SegOffsets a_seg, int64_t a_seg_len, int64_t lda,
     const uint16_t* __restrict__ bt, int64_t ldb, uint16_t* __restrict__ c, int64_t ldc,
     int64_t M, int64_t N, int64_t K, const uint16_t* __restrict__ bias,
-    int64_t a_batch_stride, int64_t c_batch_stride) {
+    int64_t a_batch_stride, int64_t c_batch_stride, PoolOut po = PoolOut()) {
   __shared__ __attribute__((aligned(1024))) char lds[2 * big::kStageB];
   // 1-D grid over (batch, m tile, n tile), n fastest.  Workgroup ids are dealt to the 8
   // XCDs round-robin; remap so each XCD gets a contiguous run of tiles and the n tiles
@@ -273,7 +301,7 @@ __global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
   if (t < full) t = (t & 7) * (full >> 3) + (t >> 3);
   const int bx = t % tn, by = (t / tn) % tm, bz = t / (tn * tm);
   a += int64_t(bz) * a_batch_stride;
-  c += int64_t(bz) * c_batch_stride;
+  if (!kPool) c += int64_t(bz) * c_batch_stride;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t m0 = int64_t(by) * big::kBM, n0 = int64_t(bx) * big::kBN;
@@ -400,14 +428,59 @@ __global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
   const int cl = lane & 15;
   const int64_t n = n0 + wn + 8 * cl;
   const bool vec_c = n + 7 < N;
+  // kPool: the pool slot of each of this lane's 16 rows (loads issued together)
+  int64_t slot_q[kPool ? big::kTM / 4 : 1];
+  if constexpr (kPool) {
+    const int32_t* btz = po.block_tables + int64_t(bz) * po.bt_stride;
+    const int bmask = (1 << po.log2_bs) - 1;
+#pragma unroll
+    for (int q = 0; q < big::kTM / 4; ++q) {
+      const int64_t m = min<int64_t>(m0 + wm + 4 * q + (lane >> 4), M - 1);
+      slot_q[q] = (int64_t(btz[m >> po.log2_bs]) << po.log2_bs) | (m & bmask);
+    }
+  }
+  // kRope: this lane's 8 columns are dims d0 .. d0 + 7 of one head; the partner chunk (half
+  // a head away) is chunk cl ^ (head_dim / 16) of the same wave tile (tiles are head-aligned)
+  const int hd = kRope ? po.head_dim : 8;
+  const int d0 = int((n0 + wn + 8 * cl) % hd);
+  const bool first_half = d0 < hd / 2;
+  const int pcl = cl ^ (hd / 16);
 #pragma unroll
   for (int q = 0; q < big::kTM / 4; ++q) {
     const int r = 4 * q + (lane >> 4);
-    const dsp_u32x4 v =
+    dsp_u32x4 v =
         *reinterpret_cast<const dsp_u32x4*>(ct + r * (big::kTN * 2) + ((cl ^ (r & 15)) * 16));
     const int64_t m = m0 + wm + r;
     if (m >= M) continue;
-    uint16_t* dst = c + m * ldc + n;
+    if constexpr (kRope) {
+      const dsp_u32x4 vp =
+          *reinterpret_cast<const dsp_u32x4*>(ct + r * (big::kTN * 2) + ((pcl ^ (r & 15)) * 16));
+      const float* cr = po.rope_cos + m * hd + d0;
+      const float* sr = po.rope_sin + m * hd + d0;
+      const f32x4 c0 = *reinterpret_cast<const f32x4*>(cr), c1 = *reinterpret_cast<const f32x4*>(cr + 4);
+      const f32x4 s0 = *reinterpret_cast<const f32x4*>(sr), s1 = *reinterpret_cast<const f32x4*>(sr + 4);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float clo = w < 2 ? c0[2 * w] : c1[2 * w - 4], chi = w < 2 ? c0[2 * w + 1] : c1[2 * w - 3];
+        const float slo = w < 2 ? s0[2 * w] : s1[2 * w - 4], shi = w < 2 ? s0[2 * w + 1] : s1[2 * w - 3];
+        const uint16_t lo = dsp_f32_to_bf16(
+            rope_apply1(dsp_bf16lo(v[w]), dsp_bf16lo(vp[w]), clo, slo, first_half));
+        const uint16_t hi = dsp_f32_to_bf16(
+            rope_apply1(dsp_bf16hi(v[w]), dsp_bf16hi(vp[w]), chi, shi, first_half));
+        v[w] = uint32_t(lo) | (uint32_t(hi) << 16);
+      }
+    }
+    uint16_t* dst;
+    if constexpr (kPool) {
+      const int64_t slot = slot_q[q];
+      if (slot < 0 || slot >= po.num_slots) {
+        if (cl == 0 && po.err_count) atomicAdd(po.err_count, 1);
+        continue;
+      }
+      dst = c + slot * ldc + n;
+    } else {
+      dst = c + m * ldc + n;
+    }
     if (vec_c && dsp_aligned(dst, 16)) {
       dsp_u32x4 w = v;
       if (kAccum) {
@@ -547,6 +620,75 @@ extern "C" int dsp_kv_map_gemm(const void* a, const int64_t* a_segment_offsets,
     map_gemm_kernel<false><<<grid, kThreads, 0, s>>>(ah, seg, segment_len, lda, bh, ldb, ch, ldc,
                                                      M, N, K, biash, bias_mode, activation,
                                                      accumulate, a_batch_stride, c_batch_stride);
+  return dsp_launch_status();
+}
+
+extern "C" int dsp_kv_map_gemm_to_pool(
+    const void* a, const int64_t* a_segment_offsets, int32_t num_segments, int64_t segment_len,
+    int64_t lda, const void* bt, int64_t ldb, void* pool, int64_t pool_row_stride,
+    int64_t num_slots, const int32_t* block_tables, int64_t bt_stride, int32_t block_size,
+    int64_t M, int64_t N, int64_t K, int32_t batch, int64_t a_batch_stride, const void* bias,
+    const float* rope_cos, const float* rope_sin, int32_t head_dim, int32_t dtype,
+    int32_t* err_count, dsp_stream_t stream) {
+  DSP_HOST_CHECK(a && bt && pool && a_segment_offsets && block_tables, DSP_EINVAL);
+  DSP_HOST_CHECK(M >= 0 && N > 0 && K > 0 && lda >= 0 && ldb >= K && pool_row_stride >= N &&
+                     num_slots >= 0 && bt_stride >= 0,
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(num_segments >= 1 && num_segments <= kMaxSegments && segment_len > 0 &&
+                     int64_t(num_segments) * segment_len == K,
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(dsp_is_pow2(block_size) && bt_stride * block_size >= M, DSP_EINVAL);
+  DSP_HOST_CHECK((rope_cos == nullptr) == (rope_sin == nullptr), DSP_EINVAL);
+  DSP_HOST_CHECK(dtype == DSP_BF16, DSP_EUNSUPPORTED);
+  DSP_HOST_CHECK(batch >= 0 && batch <= 65535 && a_batch_stride >= 0, DSP_EINVAL);
+  if (M == 0 || batch == 0) return DSP_OK;
+  const bool rope = rope_cos != nullptr;
+  // one head per 128-column wave tile (or two of 64): tiles are head-aligned
+  DSP_HOST_CHECK(!rope || ((head_dim == 64 || head_dim == 128) && N % head_dim == 0 &&
+                           dsp_aligned(rope_cos, 16) && dsp_aligned(rope_sin, 16)),
+                 DSP_EUNSUPPORTED);
+  SegOffsets seg{};
+  int64_t max_a_off = 0;
+  bool ok = dsp_aligned(a, 16) && dsp_aligned(bt, 16) && dsp_aligned(pool, 16) && lda % 8 == 0 &&
+            ldb % 8 == 0 && a_batch_stride % 8 == 0 && pool_row_stride % 8 == 0 && N % 8 == 0 &&
+            K % big::kBK == 0 && segment_len % big::kBK == 0;
+  for (int i = 0; i < num_segments; ++i) {
+    seg.off[i] = a_segment_offsets[i];
+    ok = ok && seg.off[i] % 8 == 0;
+    max_a_off = max(max_a_off, seg.off[i]);
+  }
+  // the large-tile kernel's preconditions (16-byte operand rows, 64-wide K stages, 32-bit
+  // element offsets); nothing else carries this epilogue
+  const int64_t tiles = ((M + big::kBM - 1) / big::kBM) * ((N + big::kBN - 1) / big::kBN) * batch;
+  DSP_HOST_CHECK(ok && tiles < (int64_t(1) << 31) &&
+                     max_a_off + (M - 1) * lda + segment_len <= int64_t(UINT32_MAX) &&
+                     (N - 1) * ldb + K <= int64_t(UINT32_MAX),
+                 DSP_EUNSUPPORTED);
+  PoolOut po;
+  po.block_tables = block_tables;
+  po.bt_stride = bt_stride;
+  po.log2_bs = dsp_log2i(block_size);
+  po.num_slots = num_slots;
+  po.rope_cos = rope_cos;
+  po.rope_sin = rope_sin;
+  po.head_dim = head_dim;
+  po.err_count = err_count;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const unsigned grid = static_cast<unsigned>(tiles);
+  const uint16_t* ah = static_cast<const uint16_t*>(a);
+  const uint16_t* bh = static_cast<const uint16_t*>(bt);
+  uint16_t* ch = static_cast<uint16_t*>(pool);
+  const uint16_t* biash = static_cast<const uint16_t*>(bias);
+#define DSP_POOL(B, R)                                                                    \
+  map_gemm_big_kernel<B, 0, 0, R, 1><<<grid, big::kNT, 0, s>>>(                            \
+      ah, seg, segment_len, lda, bh, ldb, ch, pool_row_stride, M, N, K, biash, a_batch_stride, \
+      0, po)
+  if (bias) {
+    if (rope) DSP_POOL(1, 1); else DSP_POOL(1, 0);
+  } else {
+    if (rope) DSP_POOL(0, 1); else DSP_POOL(0, 0);
+  }
+#undef DSP_POOL
   return dsp_launch_status();
 }
 

@@ -178,6 +178,48 @@ class LayerMap:
                   a_batch_stride=rows * hid, c_batch_stride=c_batch_stride)
         return out
 
+    def apply_to_pool(self, a: torch.Tensor, seg_offsets: list[int], seg_len: int, lda: int,
+                      rows: int, pool_layer: torch.Tensor, block_table: torch.Tensor,
+                      block_size: int, rope: tuple[torch.Tensor, torch.Tensor] | None = None,
+                      batch: int = 1, a_batch_stride: int = 0,
+                      err: torch.Tensor | None = None) -> bool:
+        """apply_into, then (keys) RoPE with the target tables, then the scatter of each
+        problem's rows into its blocks of one pool layer -- one GEMM launch writing straight
+        into the pool (dsp_kv_map_gemm_to_pool).  Returns False, having done nothing, when
+        this map or shape has no fused form (residual maps; shapes the large-tile GEMM does
+        not take): the caller then runs apply_into + RoPE + scatter."""
+        self._prepare()
+        if self.residual is not None:
+            return False
+        N = self._b.shape[0]
+        H, D = pool_layer.shape[-2], pool_layer.shape[-1]
+        if H * D != N or pool_layer.stride(-1) != 1 or pool_layer.stride(-2) != D:
+            return False
+        if self.factors is not None:
+            r = self._lt.shape[0]
+            tmp = torch.empty((batch, rows, r), dtype=torch.bfloat16, device=a.device)
+            _gemm(a, seg_offsets, seg_len, lda, rows, self._lt, tmp, batch=batch,
+                  a_batch_stride=a_batch_stride, c_batch_stride=rows * r)
+            a, seg_offsets, seg_len, lda, a_batch_stride, bt = tmp, [0], r, r, rows * r, self._rt
+        else:
+            bt = self._wt
+        cos, sin = (None, None) if rope is None else (rope[0].float().contiguous(),
+                                                      rope[1].float().contiguous())
+        if cos is not None and tuple(cos.shape) != (rows, D):
+            raise ValueError(f"rope tables {tuple(cos.shape)} do not match {rows} rows of "
+                             f"head_dim {D}")
+        offs = (ctypes.c_int64 * len(seg_offsets))(*seg_offsets)
+        st = _lib.lib().dsp_kv_map_gemm_to_pool(
+            a.data_ptr(), offs, len(seg_offsets), seg_len, lda, bt.data_ptr(), bt.stride(0),
+            pool_layer.data_ptr(), pool_layer.stride(0), pool_layer.shape[0],
+            block_table.data_ptr(), block_table.stride(0), block_size, rows, N, bt.shape[1],
+            batch, a_batch_stride, self._b.data_ptr(), _lib.ptr(cos), _lib.ptr(sin), D,
+            _lib.DSP_BF16, _lib.ptr(err), _lib.stream_of(pool_layer))
+        if st == _lib.DSP_EUNSUPPORTED:
+            return False
+        _lib.check(st, "dsp_kv_map_gemm_to_pool")
+        return True
+
     def apply(self, x: torch.Tensor, use_residual: bool = True) -> torch.Tensor:
         """y = x @ W + b (+ up(gelu(down(x)))) for x (T, K) bf16 on the GPU (:104-112)."""
         _lib.require_gpu(x)
@@ -246,6 +288,18 @@ def _stack_problems(kind: str, maps: list[LayerMap], n_src: int, n_tgt: int, kv_
                                          or m.residual[2].shape[0] != kv_dim):
             yield (f"{kind} residual for target layer {layer} does not match a "
                    f"{rows}->{kv_dim} map")
+
+
+def _scatter_one_plane(cache, layer_pool: torch.Tensor, table: torch.Tensor, cu: torch.Tensor,
+                       T: int, rows: torch.Tensor) -> None:
+    """Scatter (T, H, D) rows into one layer of one pool plane (K or V) with the import
+    kernel (dsp_kv_scatter over one layer; both of its planes name this one, so the rows
+    are written twice -- the path of maps without a fused form only)."""
+    _lib.check(_lib.lib().dsp_kv_scatter(
+        layer_pool.data_ptr(), layer_pool.data_ptr(), 1, cache.layer_bytes, cache.num_blocks,
+        cache.row_bytes, cache.block_size, table.data_ptr(), table.stride(0), cu.data_ptr(), 1,
+        T, rows.data_ptr(), rows.data_ptr(), cache._err.data_ptr(), _lib.stream_of(rows)),
+        "dsp_kv_scatter")
 
 
 class CrossModelKVMap:
@@ -332,6 +386,49 @@ class CrossModelKVMap:
         if rope is not None:
             _rope(out, rope[0], rope[1], +1, out=out)
         return out
+
+    @torch.inference_mode()
+    def map_into(self, k: torch.Tensor, v: torch.Tensor,
+                 source_rope: tuple[torch.Tensor, torch.Tensor],
+                 target_rope: tuple[torch.Tensor, torch.Tensor], cache, block_ids: list[int],
+                 use_residual: bool = True) -> None:
+        """map() followed by cache.import_contiguous(block_ids, keys, values), with each
+        target layer's GEMM writing its rows (keys re-rotated) straight into the cache's
+        blocks: no (L_tgt, T, H, D) intermediate.  Layers whose map has no fused form (a
+        trained residual) take map's path for that layer and are then scattered."""
+        _lib.require_gpu(k, v)
+        if self.dtype != torch.bfloat16:
+            raise ValueError("the HIP map runs bf16 maps (load with dtype=torch.bfloat16)")
+        L_src, T, H, D = k.shape
+        if len(self.keys) != cache.num_layers or (cache.num_kv_heads, cache.head_dim) != (H, D):
+            raise ValueError(f"a {len(self.keys)}-layer map of {H}x{D} heads cannot fill a "
+                             f"{cache.num_layers}-layer cache of {cache.num_kv_heads}x"
+                             f"{cache.head_dim}")
+        if cache.dtype != torch.bfloat16:
+            raise ValueError("map_into fills bf16 caches")
+        cache._check_blocks(block_ids, T)
+        table = cache.block_table([block_ids])
+        kv = H * D
+        content = _rope(k, *source_rope, direction=-1, out_dtype=torch.bfloat16)
+        vals = v.to(torch.bfloat16).contiguous()
+        tcos, tsin = target_rope[0].float().contiguous(), target_rope[1].float().contiguous()
+        cu = torch.tensor([0, T], dtype=torch.long).to(k.device)
+        for layer in range(cache.num_layers):
+            jobs = ((self.keys[layer], content, cache.key, (tcos, tsin)),
+                    (self.values[layer], vals, cache.value, None))
+            for m, src, pool, rope in jobs:
+                offs = [s * T * kv for s in m.source_layers]
+                if (not use_residual or m.residual is None) and m.apply_to_pool(
+                        src, offs, kv, kv, T, pool[layer], table, cache.block_size, rope,
+                        err=cache._err):
+                    continue
+                # no fused form: the map's own output, rotated, then this layer's scatter
+                out = torch.empty((T, H, D), dtype=torch.bfloat16, device=k.device)
+                m.apply_into(src, offs, kv, kv, T, out.view(T, kv), use_residual)
+                if rope is not None:
+                    _rope(out[None], tcos, tsin, +1, out=out[None])
+                _scatter_one_plane(cache, pool[layer], table, cu, T, out)
+        cache._after()
 
     @torch.inference_mode()
     def map(self, k: torch.Tensor, v: torch.Tensor,

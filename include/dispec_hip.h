@@ -298,6 +298,32 @@ int dsp_kv_map_gemm(const void* a, const int64_t* a_segment_offsets, int32_t num
                     int32_t bias_mode, int32_t activation, int32_t accumulate, int32_t dtype,
                     dsp_stream_t stream);
 
+/* J5b + J5c fused: the map GEMM writing its rows straight into a target pool layer.
+ * Replaces the tail of CrossModelKVMap._apply for one target layer -- y = x @ W + b
+ * (transfer.py:250, LayerMap.apply :104-112), keys re-rotated with the target tables in
+ * fp32 (:251-253) -- followed by PagedKVCache.import_contiguous of that layer
+ * (paged_cache.py:92-96), without the (T, KVH*D) intermediate: row m of problem z lands in
+ * pool slot block_tables[z * bt_stride + m / block_size] * block_size + m % block_size.
+ * Same A / Bt / segment / batch arguments and the same rounding as dsp_kv_map_gemm with
+ * bias_mode 1 (bias may be NULL: bf16(acc)); no activation or accumulate.
+ *   pool, pool_row_stride, num_slots : one layer of the target pool (rows of KVH*D
+ *                  elements, pool_row_stride apart); a row whose block id puts it outside
+ *                  [0, num_slots) is skipped and counted in err_count (>= 1 per such row).
+ *   rope_cos, rope_sin : fp32 [M][head_dim] tables (row m = the position of row m, shared
+ *                  by the batch) or both NULL (values: no rotation).  head_dim 64 or 128.
+ * Needs what the large-tile GEMM needs (16-byte aligned operands and rows, K and
+ * segment_len multiples of 64, N a multiple of 8 and of head_dim, 32-bit element offsets),
+ * else DSP_EUNSUPPORTED (the caller then runs dsp_kv_map_gemm + dsp_kv_rope +
+ * dsp_kv_scatter).  The result is bit-identical to that three-launch sequence. */
+int dsp_kv_map_gemm_to_pool(const void* a, const int64_t* a_segment_offsets,
+                            int32_t num_segments, int64_t segment_len, int64_t lda,
+                            const void* bt, int64_t ldb, void* pool, int64_t pool_row_stride,
+                            int64_t num_slots, const int32_t* block_tables, int64_t bt_stride,
+                            int32_t block_size, int64_t M, int64_t N, int64_t K, int32_t batch,
+                            int64_t a_batch_stride, const void* bias, const float* rope_cos,
+                            const float* rope_sin, int32_t head_dim, int32_t dtype,
+                            int32_t* err_count, dsp_stream_t stream);
+
 /* RoPE strip (direction -1) or apply (+1) on (L, T, H, D) rows in fp32:
  *     y = x * cos + direction * rotate_half(x) * sin,   rotate_half(x) = cat(-x2, x1)
  * Replaces strip_rope / apply_rope (dispec/kv/transfer.py:66-80).  cos/sin are fp32

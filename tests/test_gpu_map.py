@@ -274,3 +274,103 @@ def test_large_tile_gemm_path(B, M, N, bias_mode, act, accum):
     assert_bf16_within(bits(out.cpu()), ref_cpu.f32_to_bf16(y.astype(np.float32)),
                        bf16_chain_bound(*stages, lipschitz=1.13),
                        f"B={B} M={M} N={N} bias={bias_mode} act={act} accum={accum}")
+
+
+# ------------------------------------------- fused target RoPE + pool scatter (J5b + J5c)
+def _pool_pair(L, NB, bs, H, D, seed):
+    from dispec_amd.kv.paged_cache import PagedKVCache
+    caches = [PagedKVCache(L, NB, bs, H, D, device=DEV) for _ in range(2)]
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    for pool in (caches[0].key, caches[0].value):
+        pool.normal_(generator=g)
+    caches[1].key.copy_(caches[0].key)
+    caches[1].value.copy_(caches[0].value)
+    return caches
+
+
+@pytest.mark.parametrize("D,rope,bad_block", [(128, True, False), (128, False, False),
+                                              (64, True, False), (128, True, True)])
+def test_gemm_to_pool_equals_gemm_rope_scatter(D, rope, bad_block):
+    """dsp_kv_map_gemm_to_pool against dsp_kv_map_gemm -> dsp_kv_rope -> dsp_kv_scatter on
+    the same inputs: 3 requests of 1000 tokens (ragged against the 256-row tiles and the
+    16-token blocks), a design row of two source layers, random block placement; every
+    pool byte must match (rows outside the requests' blocks untouched by both)."""
+    from dispec_amd import _lib
+    from dispec_amd.kv.transfer import LayerMap, _gemm, _rope
+    R, Ls, T, bs = 3, 3, 1000, 16
+    H = 1024 // D
+    kv = H * D
+    g = gen(900 + D + int(rope) + 2 * int(bad_block))
+    src = torch.randn((R, Ls, T, kv), generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn((2 * kv, kv), generator=g) / 45).to(torch.bfloat16)
+    b = torch.randn(kv, generator=g).to(torch.bfloat16)
+    m = LayerMap((2, 0), b, weight=w).to(DEV, torch.bfloat16)
+    cos, sin = (torch.from_numpy(a).to(DEV) for a in ref_cpu.rope_tables(np.arange(T), D, 1e6))
+    NB = R * (-(-T // bs)) + 11
+    ref_c, got_c = _pool_pair(2, NB, bs, H, D, 77)
+    perm = torch.randperm(NB, generator=g)[:R * (-(-T // bs))].view(R, -1).to(torch.int32)
+    if bad_block:
+        perm[1, 5] = NB + 3                       # outside the pool: skipped and counted
+    table = perm.to(DEV)
+    offs = [2 * T * kv, 0]
+    # reference: dense GEMM, RoPE pass, import scatter into layer 1 (K plane)
+    dense = torch.empty((R, T, kv), dtype=torch.bfloat16, device=DEV)
+    m.apply_into(src, offs, kv, kv, T, dense, batch=R, a_batch_stride=Ls * T * kv,
+                 c_batch_stride=T * kv)
+    if rope:
+        for r in range(R):
+            _rope(dense[r].view(1, T, H, D), cos, sin, +1, out=dense[r].view(1, T, H, D))
+    err_ref = torch.zeros(1, dtype=torch.int32, device=DEV)
+    cu = torch.arange(0, (R + 1) * T, T, dtype=torch.int64, device=DEV)
+    layer = ref_c.key[1]
+    _lib.check(_lib.lib().dsp_kv_scatter(
+        layer.data_ptr(), layer.data_ptr(), 1, ref_c.layer_bytes, ref_c.num_blocks,
+        ref_c.row_bytes, bs, table.data_ptr(), table.stride(0), cu.data_ptr(), R, T,
+        dense.data_ptr(), dense.data_ptr(), err_ref.data_ptr(), _lib.stream_of(dense)), "scatter")
+    # fused
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    assert m.apply_to_pool(src, offs, kv, kv, T, got_c.key[1], table, bs,
+                           (cos, sin) if rope else None, batch=R,
+                           a_batch_stride=Ls * T * kv, err=err)
+    torch.cuda.synchronize()
+    assert torch.equal(got_c.key.view(torch.int16), ref_c.key.view(torch.int16))
+    assert torch.equal(got_c.value.view(torch.int16), ref_c.value.view(torch.int16))
+    assert (int(err.item()) > 0) == bad_block and (int(err_ref.item()) > 0) == bad_block
+
+
+@pytest.mark.parametrize("residual", [False, True])
+def test_map_into_equals_map_then_import(residual):
+    """CrossModelKVMap.map_into (fused GEMM -> pool per target layer) leaves the target cache
+    bit-identical to map() followed by import_contiguous (config-5 layer selection at a
+    small size); a map with a trained residual takes the unfused path per layer."""
+    from dispec_amd.kv.transfer import CrossModelKVMap, LayerMap
+    L_src, L_tgt, H, D, T = 6, 8, 8, 128, 300
+    kv = H * D
+    pick = lambda i: [int(round(i * (L_src - 1) / (L_tgt - 1)))]  # noqa: E731
+    maps = _maps(L_src, L_tgt, kv, 1, 31, scale=1 / 32, layer_fn=pick)
+
+    def layer_maps():
+        out = []
+        for mm in maps:
+            lm = LayerMap(mm["source_layers"], mm["bias"], weight=mm["weight"])
+            if residual:
+                g = gen(32)
+                lm.residual = (torch.randn(64, kv, generator=g) / 32, torch.randn(64, generator=g),
+                               torch.randn(kv, 64, generator=g) / 8)
+            out.append(lm.to(DEV, torch.bfloat16))
+        return out
+
+    kmap = CrossModelKVMap(layer_maps(), layer_maps(), _cfg(L_src, H, D), _cfg(L_tgt, H, D))
+    kk, vv = randn((L_src, T, H, D), 33).to(DEV), randn((L_src, T, H, D), 34).to(DEV)
+    t = lambda a: torch.from_numpy(a).to(DEV)  # noqa: E731
+    src_rope = tuple(t(a) for a in ref_cpu.rope_tables(np.arange(T), D, 1e6))
+    tgt_rope = tuple(t(a) for a in ref_cpu.rope_tables(np.arange(T), D, 5e5))
+    ref_c, got_c = _pool_pair(L_tgt, 64, 16, H, D, 35)
+    ids = torch.randperm(64, generator=gen(36))[:-(-T // 16)].tolist()
+    mk, mv = kmap.map(kk, vv, src_rope, tgt_rope)
+    ref_c.import_contiguous(ids, mk, mv)
+    kmap.map_into(kk, vv, src_rope, tgt_rope, got_c, ids)
+    torch.cuda.synchronize()
+    got_c.check_errors()
+    assert torch.equal(got_c.key.view(torch.int16), ref_c.key.view(torch.int16))
+    assert torch.equal(got_c.value.view(torch.int16), ref_c.value.view(torch.int16))
