@@ -81,4 +81,23 @@ int prefill_shared_prefix(const uint16_t* q, int64_t q_stride_t, int64_t q_strid
                           int64_t o_stride_t, int64_t o_stride_h, bool f16, int32_t* err_count,
                           hipStream_t s);
 
+// Attention for shapes outside the tuned kernels (generic_attn.hip): fp32 caches, head
+// dims 8..256 (powers of two), any GQA group.  Decode: cu_q null, max_q_len 1, one row per
+// sequence with its context clamped to [0, max_ctx]; multi-query: the semantics of
+// dsp_paged_mq_attention.  log2_bs < 0 reads `table` as a per-token slot table.  Partial
+// results need generic_workspace_bytes(B, Hq, D, max_q_len, max_ctx, P) bytes of `workspace`
+// (none for a single partition).  Grid limits: B * max_q_len <= 2^26, ceil(max_ctx / P) <=
+// 65535 (else DSP_EUNSUPPORTED).
+bool generic_head_dim(int32_t D);
+size_t generic_workspace_bytes(int32_t B, int32_t Hq, int32_t D, int32_t max_q_len,
+                               int32_t max_ctx, int32_t P);
+int generic_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                      const void* v_cache, int64_t num_slots, int64_t kv_stride_slot,
+                      int64_t kv_stride_head, const int32_t* table, int64_t table_stride,
+                      int32_t log2_bs, const int32_t* cu_q, const int32_t* ctx_lens, int32_t B,
+                      int32_t Hq, int32_t KVH, int32_t D, float scale, int32_t max_q_len,
+                      int32_t max_ctx, int32_t P, void* workspace, void* out,
+                      int64_t o_stride_t, int64_t o_stride_h, int32_t dtype, int32_t* err_count,
+                      hipStream_t s);
+
 }  // namespace dsp_detail

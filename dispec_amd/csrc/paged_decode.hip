@@ -428,7 +428,16 @@ int launch_decode(int D, int G, A... args) {
 extern "C" int dsp_paged_decode_partition_tokens(int32_t B, int32_t KVH, int32_t D,
                                                  int32_t max_ctx) {
   const int step = wg_step_for(D);
-  if (step == 0 || B <= 0 || KVH <= 0 || max_ctx <= 0) return step > 0 ? step : 0;
+  if (step == 0) {
+    if (!dsp_detail::generic_head_dim(D)) return 0;
+    // generic kernel (head dims 8 and 256): one wave per (sequence, query head, partition);
+    // 1024 keys, halved while the launch would have fewer than ~1024 x G waves
+    if (B <= 0 || KVH <= 0 || max_ctx <= 0) return 64;
+    int P = 1024;
+    while (P > 64 && int64_t(B) * KVH * ((max_ctx + P - 1) / P) < 1024) P /= 2;
+    return P;
+  }
+  if (B <= 0 || KVH <= 0 || max_ctx <= 0) return step;
   if (D == 16) {
     // VALU kernel: largest power-of-two multiple of the workgroup step, at most 512,
     // that still gives the launch enough workgroups to fill 256 CUs several times over.
@@ -493,10 +502,39 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   // a key whose block id is out of range reads row 0 instead: the cache must have one
   DSP_HOST_CHECK(num_slots > 0 || B == 0 || max_ctx == 0, DSP_EINVAL);
   DSP_HOST_CHECK(kv_stride_slot >= 0 && kv_stride_head >= 0, DSP_EINVAL);
-  DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16, DSP_EUNSUPPORTED);
+  DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16 || dtype == DSP_F32, DSP_EUNSUPPORTED);
+  DSP_HOST_CHECK(partition_tokens >= 0, DSP_EINVAL);
   const int G = Hq / KVH;
   const int step = wg_step_for(D);
-  DSP_HOST_CHECK(step > 0 && G >= 1 && G <= 8, DSP_EUNSUPPORTED);
+  if (dtype == DSP_F32 || step == 0 || G > 8) {
+    // fp32 caches, head dims outside {16, 32, 64, 128}, groups above 8: the generic kernel
+    DSP_HOST_CHECK(dsp_detail::generic_head_dim(D), DSP_EUNSUPPORTED);
+    if (B == 0) return DSP_OK;
+    const int64_t es = dtype == DSP_F32 ? 4 : 2;
+    DSP_HOST_CHECK(dsp_aligned(q, es) && dsp_aligned(k_cache, es) && dsp_aligned(v_cache, es) &&
+                       dsp_aligned(out, es),
+                   DSP_EALIGN);
+    const int32_t* tbl = block_table ? block_table : slot_table;
+    int32_t lbs = -1;
+    if (block_table) {
+      DSP_HOST_CHECK(dsp_is_pow2(block_size), DSP_EINVAL);
+      DSP_HOST_CHECK(bt_stride * block_size >= max_ctx, DSP_EINVAL);
+      lbs = dsp_log2i(block_size);
+    } else {
+      DSP_HOST_CHECK(st_stride >= max_ctx, DSP_EINVAL);
+    }
+    const int P = partition_tokens > 0 ? partition_tokens
+                                       : dsp_paged_decode_partition_tokens(B, KVH, D, max_ctx);
+    const size_t need = dsp_detail::generic_workspace_bytes(B, Hq, D, 1, max_ctx, P);
+    DSP_HOST_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+                   DSP_EWORKSPACE);
+    DSP_HOST_CHECK(need == 0 || dsp_aligned(workspace, 16), DSP_EALIGN);
+    return dsp_detail::generic_attention(
+        q, q_stride_b, q_stride_h, k_cache, v_cache, num_slots, kv_stride_slot, kv_stride_head,
+        tbl, block_table ? bt_stride : st_stride, lbs, nullptr, ctx_lens, B, Hq, KVH, D, scale,
+        1, max_ctx, P, workspace, out, o_stride_b, o_stride_h, dtype, err_count,
+        static_cast<hipStream_t>(stream));
+  }
   if (B == 0) return DSP_OK;
   // 16-byte vector loads of q and K/V rows.
   DSP_HOST_CHECK(q_stride_b % 8 == 0 && q_stride_h % 8 == 0 && kv_stride_slot % 8 == 0 &&
@@ -513,7 +551,6 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   } else {
     DSP_HOST_CHECK(st_stride >= max_ctx, DSP_EINVAL);
   }
-  DSP_HOST_CHECK(partition_tokens >= 0, DSP_EINVAL);
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const uint16_t* qh = static_cast<const uint16_t*>(q);

@@ -516,10 +516,34 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
   DSP_HOST_CHECK(B >= 0 && B <= 65535 && Hq > 0 && KVH > 0 && KVH <= 65535 && Hq % KVH == 0 &&
                      max_q_len >= 0 && max_ctx >= 0 && num_slots >= 0 && prefix_tokens >= 0,
                  DSP_EINVAL);
-  DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16, DSP_EUNSUPPORTED);
-  DSP_HOST_CHECK(D == 32 || D == 64 || D == 128, DSP_EUNSUPPORTED);
+  DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16 || dtype == DSP_F32, DSP_EUNSUPPORTED);
   DSP_HOST_CHECK(dsp_is_pow2(block_size), DSP_EINVAL);
   DSP_HOST_CHECK(bt_stride * block_size >= max_ctx, DSP_EINVAL);
+  if (dtype == DSP_F32 || !(D == 32 || D == 64 || D == 128)) {
+    // fp32 caches or head dims 8, 16, 256: the generic kernel, fixed partitions only
+    DSP_HOST_CHECK(dsp_detail::generic_head_dim(D) && prefix_tokens == 0 &&
+                       partition_tokens != DSP_SPLIT_BALANCED,
+                   DSP_EUNSUPPORTED);
+    DSP_HOST_CHECK(partition_tokens >= 0, DSP_EINVAL);
+    if (B == 0 || max_q_len == 0) return DSP_OK;
+    const int64_t es = dtype == DSP_F32 ? 4 : 2;
+    DSP_HOST_CHECK(dsp_aligned(q, es) && dsp_aligned(k_cache, es) && dsp_aligned(v_cache, es) &&
+                       dsp_aligned(out, es),
+                   DSP_EALIGN);
+    const int P = partition_tokens > 0
+                      ? partition_tokens
+                      : dsp_paged_mq_partition_tokens(B, Hq, KVH, D, max_q_len, max_ctx);
+    DSP_HOST_CHECK(P > 0 && P % 128 == 0 && (max_ctx + P - 1) / P <= kMaxParts, DSP_EINVAL);
+    const size_t need = dsp_detail::generic_workspace_bytes(B, Hq, D, max_q_len, max_ctx, P);
+    DSP_HOST_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr),
+                   DSP_EWORKSPACE);
+    DSP_HOST_CHECK(need == 0 || dsp_aligned(workspace, 16), DSP_EALIGN);
+    return dsp_detail::generic_attention(
+        q, q_stride_t, q_stride_h, k_cache, v_cache, num_slots, kv_stride_slot, kv_stride_head,
+        block_table, bt_stride, dsp_log2i(block_size), cu_q, ctx_lens, B, Hq, KVH, D, scale,
+        max_q_len, max_ctx, P, workspace, out, o_stride_t, o_stride_h, dtype, err_count,
+        static_cast<hipStream_t>(stream));
+  }
   if (B == 0 || max_q_len == 0) return DSP_OK;
   DSP_HOST_CHECK(q_stride_t % 8 == 0 && q_stride_h % 8 == 0 && kv_stride_slot % 8 == 0 &&
                      kv_stride_head % 8 == 0 && dsp_aligned(q, 16) && dsp_aligned(k_cache, 16) &&

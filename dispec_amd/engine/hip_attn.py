@@ -5,7 +5,9 @@ semantics of the reference's Triton wrappers (dispec/engine/triton_attn.py:98-13
 same argument meaning, the per-token int32 slot table, `scale = scale or D ** -0.5`, and
 an output allocated like `torch.empty_like(q)`.  They call `dsp_paged_decode`, a
 GQA-packed split-K kernel with a log-sum-exp combine, instead of one Triton program per
-(sequence, query head).
+(sequence, query head).  Like the Triton kernel they take any power-of-two head_dim from 8
+to 256 and fp32 caches as well as bf16 / fp16: shapes outside the tuned kernels (fp32, head
+dims 8 and 256, more than 8 query heads per KV head) run on a generic wave-per-row kernel.
 
 `paged_decode_attention_blocks` is the block-table form (the table is
 [B, max_blocks] int32 instead of [B, max_ctx] slots), the one `ModelRunner` uses.
@@ -17,12 +19,12 @@ import torch
 
 from dispec_amd import _lib
 
-_DTYPES = (torch.bfloat16, torch.float16)
+_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
 def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
             block_table=None, block_size=16, max_ctx=None, partition_tokens=0, out=None,
-            workspace=None):
+            workspace=None, err=None):
     _lib.require_gpu(q, k_cache, v_cache, ctx_lens)
     if q.dim() != 3 or k_cache.dim() != 3 or v_cache.shape != k_cache.shape:
         raise ValueError(f"expected q (B, Hq, D) and caches (S, KVH, D); got {tuple(q.shape)}, "
@@ -33,7 +35,7 @@ def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
         raise ValueError(f"q has {Hq} heads of {D}, cache {KVH} heads of {Dk}, kv_groups {kv_groups}")
     if q.dtype not in _DTYPES or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
         raise ValueError(f"q/k/v dtypes {q.dtype}/{k_cache.dtype}/{v_cache.dtype}: "
-                         "the HIP decode kernel takes bf16 or fp16, all the same")
+                         "the HIP decode kernels take bf16, fp16 or fp32, all the same")
     if k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
         raise ValueError("k_cache and v_cache need the same strides with head_dim contiguous")
     scale = scale or D ** -0.5
@@ -61,7 +63,8 @@ def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
         block_size, None if by_block else table.data_ptr(),
         0 if by_block else table.stride(0), ctx_lens.data_ptr(), B, Hq, KVH, D,
         float(scale), int(max_ctx), int(P), _lib.ptr(workspace), ws_bytes, out.data_ptr(),
-        out.stride(0), out.stride(1), _lib.dtype_code(q.dtype), None, _lib.stream_of(q)),
+        out.stride(0), out.stride(1), _lib.dtype_code(q.dtype), _lib.ptr(err),
+        _lib.stream_of(q)),
         "dsp_paged_decode")
     return out
 
@@ -93,17 +96,19 @@ def paged_decode_attention(q, k_cache, v_cache, slots, kv_groups, scale=None):
 
 def paged_decode_attention_blocks(q, k_cache, v_cache, block_table, ctx_lens, kv_groups,
                                   block_size=16, scale=None, max_ctx=None, partition_tokens=0,
-                                  out=None, workspace=None):
+                                  out=None, workspace=None, err=None):
     """Decode attention addressed by a block table.
 
     block_table: (B, max_blocks) int32 physical block ids; token j of sequence b lives
     in slot block_table[b, j // block_size] * block_size + j % block_size.
     max_ctx: upper bound of ctx_lens (defaults to max_blocks * block_size); it sizes the
     split-K grid, so a tight bound saves empty workgroups.
+    err: optional int32 device counter, incremented for a context length outside
+    [0, max_ctx] (clamped) and for block ids whose slots lie outside the cache (skipped).
     """
     return _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, block_table=block_table,
                    block_size=block_size, max_ctx=max_ctx, partition_tokens=partition_tokens,
-                   out=out, workspace=workspace)
+                   out=out, workspace=workspace, err=err)
 
 
 def decode_workspace(batch, num_heads, num_kv_heads, head_dim, max_ctx, device):
@@ -169,7 +174,7 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
         raise ValueError(f"q has {Hq} heads of {D}, cache {KVH} heads of {Dk}, kv_groups {kv_groups}")
     if q.dtype not in _DTYPES or k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
         raise ValueError(f"q/k/v dtypes {q.dtype}/{k_cache.dtype}/{v_cache.dtype}: "
-                         "the HIP kernels take bf16 or fp16, all the same")
+                         "the HIP kernels take bf16, fp16 or fp32, all the same")
     if k_cache.stride() != v_cache.stride() or k_cache.stride(2) != 1:
         raise ValueError("k_cache and v_cache need the same strides with head_dim contiguous")
     scale = scale or D ** -0.5

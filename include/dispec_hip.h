@@ -155,10 +155,16 @@ int dsp_kv_scatter(void* k_pool, void* v_pool, int64_t num_layers,
  *                  the combine kernel when a sequence spans more than one.  `workspace`
  *                  must hold dsp_paged_decode_workspace_bytes(..., partition_tokens)
  *                  bytes (16-byte aligned) for the same arguments, on the same device.
- * dtype: DSP_BF16 or DSP_F16.  D in {16, 32, 64, 128}; G = Hq / KVH in 1..8.
+ * dtype: DSP_BF16, DSP_F16 or DSP_F32 (caches, q and out all of it).  The tuned kernels
+ * serve bf16 / fp16 with D in {16, 32, 64, 128} and G = Hq / KVH in 1..8; every other
+ * shape with D a power of two from 8 to 256 (fp32, D 8 or 256, G above 8) runs on a
+ * generic kernel -- one wave per (sequence, query head, partition), fp32 accumulation,
+ * element-aligned pointers -- whose automatic partition is dsp_paged_decode_partition_tokens
+ * and whose workspace is covered by dsp_paged_decode_workspace_bytes.  Other D:
+ * DSP_EUNSUPPORTED.
  * err_count (optional) is incremented for a context length outside [0, max_ctx]
- * (clamped) and, on the balanced path, once per wave that met a block id whose slots lie
- * outside the cache (those keys are skipped). */
+ * (clamped) and, on the balanced and generic paths, once per wave that met a block id
+ * whose slots lie outside the cache (those keys are skipped). */
 size_t dsp_paged_decode_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
                                         int32_t max_ctx, int32_t partition_tokens);
 int dsp_paged_decode_partition_tokens(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx);
@@ -226,8 +232,11 @@ int dsp_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride
  *                faster on fixed partitions.  Needs max_q_len * G <= 16, blocks of >= 16
  *                tokens, B <= 512, D in {32, 64, 128} (else DSP_EUNSUPPORTED) and always
  *                `workspace` (dsp_paged_mq_workspace_bytes with DSP_SPLIT_BALANCED).
- * dtype DSP_BF16 / DSP_F16; D in {32, 64, 128}; any G = Hq / KVH.  A sequence with
- * q_len > ctx or ctx > max_ctx is counted in err_count and its rows written as zeros.
+ * dtype DSP_BF16 / DSP_F16 with D in {32, 64, 128} on the tuned kernels; DSP_F32, or D 8,
+ * 16 or 256, on a generic kernel (one wave per query row, head and key partition; fixed
+ * partitions only -- DSP_SPLIT_BALANCED and the shared-prefix entry return
+ * DSP_EUNSUPPORTED for them); any G = Hq / KVH.  A sequence with q_len > ctx or
+ * ctx > max_ctx is counted in err_count and its rows written as zeros.
  * Batches with max_q_len * G >= 128 (D 64 or 128, blocks of >= 16 tokens) run on a
  * 128-row tile built for chunked prefill; shorter ones (verify) on 16-row tiles.  The
  * automatic partition is sized for whichever runs. */

@@ -61,8 +61,8 @@ def test_host_argument_checks_reject_before_launch(lib):
     # empty work is a no-op success even with no device
     fake = ctypes.c_void_p(0x1000)
     assert lib.dsp_kv_append(fake, fake, 10, 16, fake, fake, 16, None, 0, 16, None, None) == 0
-    # decode: G = Hq / KVH = 9 has no kernel; a non-power-of-two block size is invalid
-    args = dict(B=1, Hq=18, KVH=2, D=64)
+    # decode: head_dim 512 has no kernel; a non-power-of-two block size is invalid
+    args = dict(B=1, Hq=18, KVH=2, D=512)
     st = lib.dsp_paged_decode(fake, 64 * 18, 64, fake, fake, 64, 128, 64, fake, 4, 16, None, 0,
                               fake, args["B"], args["Hq"], args["KVH"], args["D"], 0.125, 64, 0,
                               None, 0, fake, 64 * 18, 64, _lib.DSP_BF16, None, None)
@@ -115,4 +115,10 @@ def test_partition_and_workspace_sizing(lib):
     # a small launch: at least 4 units of 16 keys per wave -> 4*2*ceil(500/16)/4 = 64 waves
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, 0) == (4 * 2 + 64) * 7 * 66 * 4
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 3, 64, 500, 0) == 0     # 14 % 3 != 0
-    assert lib.dsp_paged_decode_workspace_bytes(1, 4, 2, 256, 64, 0) == 0      # no D=256 kernel
+    # head_dim 256 (generic kernel): 1024-token partitions halved while the launch has fewer
+    # than 1024 (sequence, KV head, partition) triples; one partition needs no workspace
+    assert lib.dsp_paged_decode_partition_tokens(16, 8, 256, 32768) == 1024
+    assert lib.dsp_paged_decode_partition_tokens(1, 2, 256, 4096) == 64
+    assert lib.dsp_paged_decode_workspace_bytes(16, 32, 8, 256, 32768, 0) == 16 * 32 * 32 * 258 * 4
+    assert lib.dsp_paged_decode_workspace_bytes(1, 4, 2, 256, 64, 0) == 0
+    assert lib.dsp_paged_decode_partition_tokens(1, 2, 512, 4096) == 0          # no D=512 kernel

@@ -168,10 +168,10 @@ def test_invalid_arguments_raise(hip):
     ctx = torch.ones(1, dtype=torch.int32, device=DEV)
     with pytest.raises(ValueError):
         paged_decode_attention_blocks(q, kc, kc, bt, ctx, 3)          # 4 != 2 * 3
-    with pytest.raises(ValueError):
-        paged_decode_attention_blocks(q.float(), kc.float(), kc.float(), bt, ctx, 2)
+    with pytest.raises(ValueError):                                    # mixed dtypes
+        paged_decode_attention_blocks(q.float(), kc, kc, bt, ctx, 2)
     with pytest.raises(ValueError):
         paged_decode_attention_blocks(q, kc, kc, bt, ctx, 2, block_size=12)
-    big = randn((64, 2, 256), 3).to(DEV)
+    big = randn((64, 2, 512), 3).to(DEV)                               # head_dim 512
     with pytest.raises(ValueError, match="no compiled kernel"):
-        paged_decode_attention_blocks(randn((1, 4, 256), 4).to(DEV), big, big, bt, ctx, 2)
+        paged_decode_attention_blocks(randn((1, 4, 512), 4).to(DEV), big, big, bt, ctx, 2)
