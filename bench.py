@@ -911,6 +911,20 @@ def bench_c5(torch) -> dict:
            "c5_scatter_GBps": 2 * 2 * Lt * R * T * tgt.row_bytes / s_s / 1e9,
            "append_prefill_GBps": 2 * 2 * n * tgt.row_bytes / a_s / 1e9,
            "append_prefill_warm_GBps": 2 * 2 * n * tgt.row_bytes / a_warm_s / 1e9}
+    # roofline objects of the config-5 kernels: gather against HBM (its bytes, read once
+    # and written once), the map launch against dense bf16 MFMA; traffic from the counter
+    # passes in profiles/byte_movers_c4_c5_traffic.md
+    movers = "byte_movers_c4_c5_traffic.md"
+    res["c5_gather_roofline"] = {
+        "bound": "hbm", "achieved": round(moved / g_s / 1e9, 1), "peak": PEAK_HBM_GBPS,
+        "unit": "GB/s", "frac": round(moved / g_s / 1e9 / PEAK_HBM_GBPS, 4),
+        "traffic": _traffic_per_launch(movers, "c5_gather"), "alg_bytes_per_launch": moved}
+    per_launch = m_s / (2 * len(maps))
+    res["c5_map_roofline"] = {
+        "bound": "mfma", "achieved": round(flops / m_s / 1e12, 1), "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s", "frac": round(flops / m_s / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "traffic": _traffic_per_launch(movers, "c5_map"),
+        "flops_per_launch": flops / (2 * len(maps)), "us_per_launch": round(per_launch * 1e6, 2)}
     del tgt, kbuf, vbuf, mk, mv
     torch.cuda.empty_cache()
     return res
@@ -951,17 +965,18 @@ def bench_copy_ceiling(torch) -> dict:
     return {"copy_ceiling_GBps": 2 * n / best / 1e9}
 
 
-def _traffic_per_launch():
-    """HBM bytes per decode launch (FETCH_SIZE + WRITE_SIZE of the balanced decode kernel
-    and its combine, each scaled by the copy calibration), as measured by the rocprofv3
-    passes recorded in profiles/decode_c3_traffic.md; None if absent."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "decode_c3_traffic.md")
+def _traffic_per_launch(profile="decode_c3_traffic.md", key=""):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, each scaled by the copy calibration)
+    as measured by the rocprofv3 passes recorded in profiles/<profile>: the line
+    `traffic_bytes_per_launch:` (decode: the balanced decode kernel and its combine) or
+    `traffic_bytes_per_launch[<key>]:`; None if absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", profile)
     if not os.path.exists(path):
         return None
+    tag = f"traffic_bytes_per_launch[{key}]:" if key else "traffic_bytes_per_launch:"
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":")[1])
+        if line.startswith(tag):
+            return int(line[len(tag):].split()[0])
     return None
 
 
