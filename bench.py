@@ -83,7 +83,9 @@ def _probe_lib():
         sigs = {"dsp_probe_stream_read": [P, c_int64, c_int32, P, P],
                 "dsp_probe_stream_copy": [P, P, c_int64, c_int32, P],
                 "dsp_probe_slice_read": [P, P, c_int64, P, c_int64, c_int32, c_int32, c_int32,
-                                         c_int32, c_int32, P, P]}
+                                         c_int32, c_int32, P, P],
+                "dsp_probe_gemm_fill": [P, c_int64, c_int64, c_int64, P, c_int64, c_int64,
+                                        c_int64, c_int32, P, P]}
         for name, args in sigs.items():
             fn = getattr(lib, name)
             fn.restype, fn.argtypes = c_int, args
@@ -832,6 +834,7 @@ def bench_c5(torch) -> dict:
     buffers, map each of 36 target layers from source layer round(i*27/35) with a bf16
     1024x1024 map (weights ~N(0, 1/1024)) for K and V, scatter into a randomly placed
     Qwen3-4B-layout pool (36 L)."""
+    from dispec_amd import _lib
     from dispec_amd.kv.paged_cache import PagedKVCache
     from dispec_amd.kv.transfer import LayerMap
 
@@ -876,6 +879,18 @@ def bench_c5(torch) -> dict:
 
     m_s = _time_gpu(torch, run_map, 3, warmup=1)
     flops = 2 * 2 * Lt * R * T * kv * kv
+    # the floor of one map launch: its operand stages loaded into LDS with no arithmetic
+    # (dsp_probe_gemm_fill: same tiles, same order, same loads)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    probe = _probe_lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def fill_probe():
+        _lib.check(probe.dsp_probe_gemm_fill(kbuf.data_ptr(), kv, T, Ls * T * kv,
+                                             w_probe.data_ptr(), kv, kv, kv, R,
+                                             sink.data_ptr(), stream), "probe")
+    w_probe = torch.empty((kv, kv), dtype=torch.bfloat16, device=dev).normal_()
+    fill_s = _time_gpu(torch, fill_probe, 20)
     # scatter into a 36-layer target pool
     tgt = PagedKVCache(Lt, NB, bs, KVH, D, device=dev)
     perm = torch.randperm(NB, generator=gcpu)[:nb].view(R, T // bs)
@@ -920,6 +935,8 @@ def bench_c5(torch) -> dict:
         "unit": "GB/s", "frac": round(moved / g_s / 1e9 / PEAK_HBM_GBPS, 4),
         "traffic": _traffic_per_launch(movers, "c5_gather"), "alg_bytes_per_launch": moved}
     per_launch = m_s / (2 * len(maps))
+    res["c5_map_fill_floor_us"] = round(fill_s * 1e6, 2)
+    res["c5_map_us_per_launch"] = round(per_launch * 1e6, 2)
     res["c5_map_roofline"] = {
         "bound": "mfma", "achieved": round(flops / m_s / 1e12, 1), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(flops / m_s / 1e12 / PEAK_BF16_TFLOPS, 4),

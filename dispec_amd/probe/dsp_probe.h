@@ -36,6 +36,12 @@ int dsp_probe_slice_read(const void* k_cache, const void* v_cache, int64_t num_s
                          const int32_t* block_table, int64_t bt_stride, int32_t block_size,
                          int32_t B, int32_t KVH, int32_t ctx, int32_t waves_per_seq_head,
                          uint32_t* sink, dsp_stream_t stream);
+/*   dsp_probe_gemm_fill: the loads of one map_gemm_big_kernel launch (C = A . Bt^T, batch
+ *     problems of M x N x K, A rows lda apart, problem z's A at a + z * a_batch_stride) into
+ *     LDS stages, with no MFMA and no epilogue: the floor of that launch's time. */
+int dsp_probe_gemm_fill(const void* a, int64_t lda, int64_t M, int64_t a_batch_stride,
+                        const void* bt, int64_t ldb, int64_t N, int64_t K, int32_t batch,
+                        uint32_t* sink, dsp_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,6 +1,7 @@
 // Bandwidth probes for the roofline: what this GPU's HBM delivers to (1) a plain streaming
-// read, (2) a read with the paged decode's access pattern, with no compute, and (3) a plain
-// streaming copy (the ceiling of the append / gather / scatter / block-copy kernels).
+// read, (2) a read with the paged decode's access pattern, with no compute, (3) a plain
+// streaming copy (the ceiling of the append / gather / scatter / block-copy kernels), and
+// (4) the map GEMM's operand stages into LDS with no MFMA and no epilogue.
 // They calibrate the decode kernel's measured GB/s: the datasheet peak (8 TB/s) is not
 // reachable by any read, and the slot-major pool layout (one KV head's 256-byte slice of
 // every 2 KiB slot row) caps what the decode can fetch below a streaming read.  Both probes
@@ -95,6 +96,56 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(const dsp_u32x4* __res
   }
 }
 
+// The map GEMM's loads without its arithmetic: the same 256 x 256 tiles in the same
+// XCD-aware order, each 64-wide K stage of 256 A rows and 256 Bt rows (128 bytes each)
+// going straight into LDS with global_load_lds_dwordx4, two stages resident, one barrier
+// per stage -- what one launch of map_gemm_big_kernel needs just to fill its stages.
+__global__ __launch_bounds__(512) void gemm_fill_kernel(const uint16_t* __restrict__ a, int64_t lda,
+                                                        int64_t M, int64_t a_batch_stride,
+                                                        const uint16_t* __restrict__ bt, int64_t ldb,
+                                                        int64_t N, int64_t K,
+                                                        uint32_t* __restrict__ sink) {
+  constexpr int kBM = 256, kBN = 256, kBK = 64, kCPR = 8, kRowB = 128, kLPW = 8;
+  constexpr int kStageB = (kBM + kBN) * kRowB;
+  __shared__ __attribute__((aligned(1024))) char lds[2 * kStageB];
+  const int tn = int((N + kBN - 1) / kBN), tm = int((M + kBM - 1) / kBM);
+  int t = int(blockIdx.x);
+  const int full = int(gridDim.x) & ~7;
+  if (t < full) t = (t & 7) * (full >> 3) + (t >> 3);
+  const int bx = t % tn, by = (t / tn) % tm, bz = t / (tn * tm);
+  a += int64_t(bz) * a_batch_stride;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t m0 = int64_t(by) * kBM, n0 = int64_t(bx) * kBN;
+  const bool loads_a = wave * kLPW * 64 < kBM * kCPR;
+  uint32_t off[kLPW];
+#pragma unroll
+  for (int j = 0; j < kLPW; ++j) {
+    const int r = (wave * kLPW + j) * (64 / kCPR) + lane / kCPR;
+    const int chunk = (lane % kCPR) ^ (r & 7);
+    const int64_t row = loads_a ? min<int64_t>(m0 + r, M - 1) : min<int64_t>(n0 + r - kBM, N - 1);
+    off[j] = uint32_t(row * (loads_a ? lda : ldb) + chunk * 8);
+  }
+  auto issue = [&](int buf, int64_t k0) {
+    const uint16_t* src = (loads_a ? a : bt) + k0;
+    char* dst = lds + buf * kStageB + wave * kLPW * 1024;
+#pragma unroll
+    for (int j = 0; j < kLPW; ++j)
+      __builtin_amdgcn_global_load_lds(static_cast<const void*>(src + off[j]),
+                                       (__attribute__((address_space(3))) void*)(dst + j * 1024),
+                                       16, 0, 0);
+  };
+  const int nk = int(K / kBK);
+  issue(0, 0);
+  uint32_t h = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    __syncthreads();  // stage kt landed; every wave is past its read of stage kt - 1
+    h ^= *reinterpret_cast<const uint32_t*>(lds + (kt & 1) * kStageB + threadIdx.x * 4);
+    if (kt + 1 < nk) issue((kt + 1) & 1, int64_t(kt + 1) * kBK);
+  }
+  if (h == 0x9e3779b9u) sink[0] = h;
+}
+
 }  // namespace
 
 extern "C" int dsp_probe_stream_copy(const void* src, void* dst, int64_t bytes,
@@ -147,5 +198,23 @@ extern "C" int dsp_probe_slice_read(const void* k_cache, const void* v_cache, in
     slice_read_kernel<1><<<dim3(static_cast<unsigned>(grid)), 64, 0, st>>>(
         kh, vh, num_slots, block_table, bt_stride, dsp_log2i(block_size), KVH,
         ctx / waves_per_seq_head, waves_per_seq_head, sink);
+  return dsp_launch_status();
+}
+
+extern "C" int dsp_probe_gemm_fill(const void* a, int64_t lda, int64_t M, int64_t a_batch_stride,
+                                   const void* bt, int64_t ldb, int64_t N, int64_t K,
+                                   int32_t batch, uint32_t* sink, dsp_stream_t stream) {
+  DSP_HOST_CHECK(a && bt && sink && M > 0 && N > 0 && batch > 0, DSP_EINVAL);
+  DSP_HOST_CHECK(K > 0 && K % 64 == 0 && lda >= K && ldb >= K && lda % 8 == 0 && ldb % 8 == 0 &&
+                     a_batch_stride % 8 == 0,
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(dsp_aligned(a, 16) && dsp_aligned(bt, 16), DSP_EALIGN);
+  DSP_HOST_CHECK((M - 1) * lda + K <= int64_t(UINT32_MAX) && (N - 1) * ldb + K <= int64_t(UINT32_MAX),
+                 DSP_EINVAL);
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256) * batch;
+  DSP_HOST_CHECK(tiles < (int64_t(1) << 31), DSP_EINVAL);
+  gemm_fill_kernel<<<dim3(static_cast<unsigned>(tiles)), 512, 0, static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(a), lda, M, a_batch_stride, static_cast<const uint16_t*>(bt), ldb,
+      N, K, sink);
   return dsp_launch_status();
 }
