@@ -121,6 +121,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   // in LDS first, so a key's slot costs an LDS read rather than a dependent global load.
   const int bmask = (1 << log2_bs) - 1;
   int win_blk = 0;  // first block of the staged window
+  bool any_bad = false;  // a visible key's block id put it outside the cache (skipped)
   auto slot_of = [&](int key) -> int64_t {
     const int64_t sl = int64_t(s_blk[(key >> log2_bs) - win_blk]) * (bmask + 1) + (key & bmask);
     return (sl >= 0 && sl < num_slots) ? sl : -1;
@@ -139,6 +140,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     for (int st = 0; st < 2; ++st) {
       const int key = t0 + 16 * st + n;
       const int64_t s = key < kfin ? slot_of(key) : -1;
+      any_bad |= key < kfin && s < 0;
 #pragma unroll
       for (int kk = 0; kk < NKK; ++kk)
         kop[st][kk] = s >= 0 ? *reinterpret_cast<const dsp_u32x4*>(kc + s * kvs_slot + head_off +
@@ -255,6 +257,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
     pending = prefetch;
   }
 
+  // counted once per wave that met an out-of-range block id
+  if (err_count && __ballot(any_bad) && lane == 0) atomicAdd(err_count, 1);
   // Row sums: this lane's keys only so far; add the other three lane groups.
   lpart += dsp_shfl_xor(lpart, 16);
   lpart += dsp_shfl_xor(lpart, 32);

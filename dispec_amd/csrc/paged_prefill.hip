@@ -236,10 +236,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   auto load_blk = [&](int t0) {
     return bt[bt_row + (min(t0 + 16 * wave, kfin - 1) >> log2_bs)];
   };
+  bool any_bad = false;  // (wave-uniform) a block id of visible keys lay outside the cache
   auto issue = [&](int buf, int t0, int32_t blk_v) {
     const int32_t blk = __builtin_amdgcn_readfirstlane(blk_v);
     int64_t slot0 = int64_t(blk) * (bmask + 1) + ((t0 + 16 * wave) & bmask);
-    if (blk < 0 || (int64_t(blk) + 1) * (bmask + 1) > num_slots) slot0 = 0;
+    if (blk < 0 || (int64_t(blk) + 1) * (bmask + 1) > num_slots) {
+      slot0 = 0;
+      any_bad |= t0 + 16 * wave < kfin;
+    }
     const int64_t e = slot0 * kvs_slot + head_off;
     const char* kb = reinterpret_cast<const char*>(kc + e);
     const char* vb = reinterpret_cast<const char*>(vc + e);
@@ -366,6 +370,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
       }
     }
   }
+
+  if (err_count && any_bad && lane == 0) atomicAdd(err_count, 1);  // once per wave
 
   // ---- epilogue: row sums over the two lane halves; acc[dt][j] = O[row col][dim 32*dt +
   // 8*(j/4) + 4*hl + j%4]

@@ -163,7 +163,7 @@ int dsp_kv_scatter(void* k_pool, void* v_pool, int64_t num_layers,
  * and whose workspace is covered by dsp_paged_decode_workspace_bytes.  Other D:
  * DSP_EUNSUPPORTED.
  * err_count (optional) is incremented for a context length outside [0, max_ctx]
- * (clamped) and, on the balanced and generic paths, once per wave that met a block id
+ * (clamped) and, on block tables and the generic kernel, once per wave that met a block id
  * whose slots lie outside the cache (those keys are skipped). */
 size_t dsp_paged_decode_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
                                         int32_t max_ctx, int32_t partition_tokens);
@@ -236,7 +236,10 @@ int dsp_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride
  * 16 or 256, on a generic kernel (one wave per query row, head and key partition; fixed
  * partitions only -- DSP_SPLIT_BALANCED and the shared-prefix entry return
  * DSP_EUNSUPPORTED for them); any G = Hq / KVH.  A sequence with q_len > ctx or
- * ctx > max_ctx is counted in err_count and its rows written as zeros.
+ * ctx > max_ctx is counted in err_count and its rows written as zeros.  A block id whose
+ * slots lie outside the cache is never dereferenced: it is counted once per wave that met
+ * it, and its keys are masked out on the 16-row tiles and the balanced split, read from
+ * slots 0..15 on the 128-row tile (that sequence's result is then unspecified).
  * Batches with max_q_len * G >= 128 (D 64 or 128, blocks of >= 16 tokens) run on a
  * 128-row tile built for chunked prefill; shorter ones (verify) on 16-row tiles.  The
  * automatic partition is sized for whichever runs. */

@@ -142,6 +142,18 @@ def test_balanced_matches_fixed_partitions(hip):
     assert_attention_close(f64(bal), f64(fixed), "balanced vs fixed")
 
 
+@pytest.mark.parametrize("KVH,G,D", [(8, 4, 128), (2, 6, 128), (1, 7, 64), (4, 2, 32)])
+@pytest.mark.parametrize("P", [64, 192, 512])
+def test_fixed_partitions_on_head_groups(hip, KVH, G, D, P):
+    """Explicit partitions on block tables: one worker of the balanced kernel per
+    (sequence, group of KV heads, partition).  Contexts of 0 and 1 tokens, exact multiples
+    of P, one key past a multiple, one partition short of one, and several partitions."""
+    lens = [0, 1, P, P + 1, P - 16, 5 * P + 7, 3 * P, 33]
+    out, ref = _run(lens, KVH, G, D, 16, 2100 + P + D, partition_tokens=P)
+    assert_attention_close(f64(out), ref, f"KVH={KVH} G={G} D={D} P={P}")
+    assert not out[0].any()                      # ctx 0 writes zeros
+
+
 @pytest.mark.parametrize("B", [512, 513])
 def test_largest_batch_and_fallback(hip, B):
     """512 sequences is the largest batch the balanced split serves; 513 falls back to
@@ -151,31 +163,32 @@ def test_largest_batch_and_fallback(hip, B):
     assert_attention_close(f64(out), ref, f"B={B}")
 
 
-def _raw_decode(q, kc, vc, bt, ctx, KVH, G, bs, max_ctx, err):
+def _raw_decode(q, kc, vc, bt, ctx, KVH, G, bs, max_ctx, err, P=0):
     from dispec_amd import _lib
     L = _lib.lib()
     B, Hq, D = q.shape
-    need = L.dsp_paged_decode_workspace_bytes(B, Hq, KVH, D, max_ctx, 0)
+    need = L.dsp_paged_decode_workspace_bytes(B, Hq, KVH, D, max_ctx, P)
     ws = torch.empty(need // 4 + 1, dtype=torch.float32, device=DEV)
     out = torch.full_like(q, float("nan"))
     _lib.check(L.dsp_paged_decode(q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(),
                                   vc.data_ptr(), kc.shape[0], kc.stride(0), kc.stride(1),
                                   bt.data_ptr(), bt.stride(0), bs, None, 0, ctx.data_ptr(), B,
-                                  Hq, KVH, D, D ** -0.5, max_ctx, 0, ws.data_ptr(),
+                                  Hq, KVH, D, D ** -0.5, max_ctx, P, ws.data_ptr(),
                                   ws.numel() * 4, out.data_ptr(), out.stride(0), out.stride(1),
                                   _lib.DSP_BF16, err.data_ptr(), _lib.stream_of(q)), "decode")
     torch.cuda.synchronize()
     return out
 
 
-def test_bad_lengths_are_clamped_and_counted(hip):
+@pytest.mark.parametrize("P", [0, 64])
+def test_bad_lengths_are_clamped_and_counted(hip, P):
     KVH, G, D, bs = 2, 2, 64, 16
     kc, vc = randn((64, KVH, D), 1900).to(DEV), randn((64, KVH, D), 1901).to(DEV)
     q = randn((3, KVH * G, D), 1902).to(DEV)
     bt = torch.tensor([[0, 1], [2, 3], [0, 3]], dtype=torch.int32).to(DEV)
     err = torch.zeros(1, dtype=torch.int32, device=DEV)
     ctx = torch.tensor([40, -3, 20], dtype=torch.int32, device=DEV)
-    out = _raw_decode(q, kc, vc, bt, ctx, KVH, G, bs, 32, err)
+    out = _raw_decode(q, kc, vc, bt, ctx, KVH, G, bs, 32, err, P)
     assert int(err.item()) == 2
     assert torch.count_nonzero(out[1]) == 0          # negative length: empty context
     tables = [[0, 1], [2, 3], [0, 3]]
@@ -184,14 +197,15 @@ def test_bad_lengths_are_clamped_and_counted(hip):
     assert_attention_close(f64(out), ref, "clamped")
 
 
-def test_out_of_range_block_ids_are_counted_not_read(hip):
+@pytest.mark.parametrize("P", [0, 64])
+def test_out_of_range_block_ids_are_counted_not_read(hip, P):
     KVH, G, D, bs = 2, 2, 64, 16
     kc, vc = randn((64, KVH, D), 2000).to(DEV), randn((64, KVH, D), 2001).to(DEV)
     q = randn((2, KVH * G, D), 2002).to(DEV)
     bt = torch.tensor([[0, 1], [2, 1 << 20]], dtype=torch.int32).to(DEV)
     err = torch.zeros(1, dtype=torch.int32, device=DEV)
     ctx = torch.tensor([20, 20], dtype=torch.int32, device=DEV)
-    out = _raw_decode(q, kc, vc, bt, ctx, KVH, G, bs, 32, err)
+    out = _raw_decode(q, kc, vc, bt, ctx, KVH, G, bs, 32, err, P)
     assert int(err.item()) >= 1
     assert torch.isfinite(out).all()
     ref = ref_cpu.decode_attention(f64(q[:1]), f64(kc), f64(vc), _slot_table([[0, 1]], [20], bs),

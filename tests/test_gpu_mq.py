@@ -112,3 +112,31 @@ def test_split_k_partitions_agree(P):
     slot_lists = [ref_cpu.context_slots(t, n, bs) for t, n in zip(tables, ctx)]
     ref = ref_cpu.mq_attention(f64(q), f64(kc), f64(vc), slot_lists, q_lens, Hq // KVH)
     assert_attention_close(f64(out), ref, f"P={P}")
+
+
+@pytest.mark.parametrize("q_lens", [[5, 5], [200, 200]], ids=["16-row", "128-row"])
+def test_out_of_range_block_id_is_counted_and_never_read(q_lens):
+    """A block id past the pool is never dereferenced and is counted; the other sequence
+    of the batch (on the 16-row tiles and on the 128-row prefill tile) is unaffected."""
+    from dispec_amd.engine.hip_attn import paged_mq_attention
+    bs, Hq, KVH, D, NB = 16, 16, 8, 128, 40
+    ctx = [300, 300]
+    tables = random_block_tables(NB, ctx, bs, 95)
+    kc, vc = randn((NB * bs, KVH, D), 96), randn((NB * bs, KVH, D), 97)
+    q = randn((sum(q_lens), Hq, D), 98)
+    bt = torch.zeros((2, max(len(t) for t in tables)), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t)
+    bt[1, 3] = 1 << 24                          # sequence 1: one block id past the pool
+    cu = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = paged_mq_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), cu.to(DEV),
+                             torch.tensor(ctx, dtype=torch.int32).to(DEV), Hq // KVH,
+                             block_size=bs, max_q_len=max(q_lens), err=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) >= 1
+    assert torch.isfinite(out).all()
+    ref = ref_cpu.mq_attention(f64(q[:q_lens[0]]), f64(kc), f64(vc),
+                               [ref_cpu.context_slots(tables[0], ctx[0], bs)], q_lens[:1],
+                               Hq // KVH)
+    assert_attention_close(f64(out[:q_lens[0]]), ref, f"good sequence, q_len {q_lens[0]}")
