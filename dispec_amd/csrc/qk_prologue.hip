@@ -146,6 +146,88 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(
       *reinterpret_cast<const dsp_u32x4*>(v + t * vst + int64_t(kh) * vsh + 8 * sub);
 }
 
+// fp32 models: the same prologue with 4 elements per 16-byte lane (D/4 lanes per row) and
+// no rounding between the steps (every torch op on fp32 tensors rounds to fp32, which the
+// fp32 arithmetic here does as it goes).
+template <int D>
+__global__ __launch_bounds__(256) void qk_prologue_f32_kernel(
+    const float* __restrict__ q, int64_t qst, int64_t qsh, const float* __restrict__ k,
+    int64_t kst, int64_t ksh, const float* __restrict__ v, int64_t vst, int64_t vsh,
+    const float* __restrict__ qw, const float* __restrict__ kw, float eps,
+    const float* __restrict__ cosp, const float* __restrict__ sinp, int64_t rst,
+    const int64_t* __restrict__ slots, int64_t T, int32_t Hq, int32_t KVH,
+    float* __restrict__ qo, int64_t qost, int64_t qosh, float* __restrict__ kpool,
+    float* __restrict__ vpool, int64_t num_slots, int64_t pss, int64_t psh,
+    int32_t* __restrict__ err_count) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int LPR = D / 4;       // lanes per row
+  constexpr int RPW = 64 / LPR;    // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int sub = lane % LPR;      // 4-element chunk of the row this lane holds
+  const int64_t row = (int64_t(blockIdx.x) * (blockDim.x / 64) + threadIdx.x / 64) * RPW +
+                      lane / LPR;
+  const int heads = Hq + KVH;
+  const bool live = row < T * heads;
+  const int64_t t = live ? row / heads : 0;
+  const int j = live ? static_cast<int>(row % heads) : 0;
+  const bool is_q = j < Hq;
+  const int kh = j - Hq;
+  const float* src = is_q ? q + t * qst + int64_t(j) * qsh : k + t * kst + int64_t(kh) * ksh;
+  f4 x = live ? *reinterpret_cast<const f4*>(src + 4 * sub) : f4{0.f, 0.f, 0.f, 0.f};
+  const float* w = is_q ? qw : kw;
+  if (w != nullptr) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ss = fmaf(x[i], x[i], ss);
+#pragma unroll
+    for (int m = 1; m < LPR; m <<= 1) ss += __int_as_float(static_cast<int>(shfl_xor_u32(__float_as_uint(ss), m)));
+    const float inv = rsqrtf(ss / float(D) + eps);
+    const f4 wv = *reinterpret_cast<const f4*>(w + 4 * sub);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = wv[i] * (x[i] * inv);
+  }
+  f4 pr;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) pr[i] = __uint_as_float(shfl_xor_u32(__float_as_uint(x[i]), LPR / 2));
+  const bool first_half = sub < LPR / 2;
+  const f4 cv = *reinterpret_cast<const f4*>(cosp + t * rst + 4 * sub);
+  const f4 sv = *reinterpret_cast<const f4*>(sinp + t * rst + 4 * sub);
+  f4 out;
+  {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float rot = first_half ? -pr[i] : pr[i];
+      out[i] = x[i] * cv[i] + rot * sv[i];
+    }
+  }
+  if (!live) return;
+  if (is_q) {
+    *reinterpret_cast<f4*>(qo + t * qost + int64_t(j) * qosh + 4 * sub) = out;
+    return;
+  }
+  const int64_t slot = slots[t];
+  if (slot < 0 || slot >= num_slots) {
+    if (sub == 0 && err_count) atomicAdd(err_count, 1);
+    return;
+  }
+  const int64_t pe = slot * pss + int64_t(kh) * psh + 4 * sub;
+  *reinterpret_cast<f4*>(kpool + pe) = out;
+  *reinterpret_cast<f4*>(vpool + pe) = *reinterpret_cast<const f4*>(v + t * vst + int64_t(kh) * vsh + 4 * sub);
+}
+
+template <typename... A>
+int launch_f32(int D, unsigned grid, hipStream_t s, A... args) {
+  switch (D) {
+    case 32: qk_prologue_f32_kernel<32><<<grid, 256, 0, s>>>(args...); break;
+    case 64: qk_prologue_f32_kernel<64><<<grid, 256, 0, s>>>(args...); break;
+    case 128: qk_prologue_f32_kernel<128><<<grid, 256, 0, s>>>(args...); break;
+    case 256: qk_prologue_f32_kernel<256><<<grid, 256, 0, s>>>(args...); break;
+    default: return DSP_EUNSUPPORTED;
+  }
+  return dsp_launch_status();
+}
+
 template <typename Tag, typename... A>
 int launch(int D, unsigned grid, hipStream_t s, A... args) {
   switch (D) {
@@ -170,7 +252,7 @@ extern "C" int dsp_qk_norm_rope_append(
     int64_t pool_stride_head, int32_t dtype, int32_t* err_count, dsp_stream_t stream) {
   DSP_HOST_CHECK(T >= 0 && Hq > 0 && KVH > 0 && num_slots >= 0, DSP_EINVAL);
   DSP_HOST_CHECK((q_norm_weight == nullptr) == (k_norm_weight == nullptr), DSP_EINVAL);
-  DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16, DSP_EUNSUPPORTED);
+  DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16 || dtype == DSP_F32, DSP_EUNSUPPORTED);
   DSP_HOST_CHECK(D == 32 || D == 64 || D == 128 || D == 256, DSP_EUNSUPPORTED);
   if (T == 0) return DSP_OK;
   DSP_HOST_CHECK(q && k && v && cos_table && sin_table && slots && q_out && k_pool && v_pool,
@@ -179,12 +261,13 @@ extern "C" int dsp_qk_norm_rope_append(
                      v_stride_t >= 0 && v_stride_h >= 0 && rope_stride_t >= 0 &&
                      pool_stride_slot >= 0 && pool_stride_head >= 0,
                  DSP_EINVAL);
-  // 16-byte vectors: every row start and every stride a multiple of 8 elements
-  DSP_HOST_CHECK(q_stride_t % 8 == 0 && q_stride_h % 8 == 0 && k_stride_t % 8 == 0 &&
-                     k_stride_h % 8 == 0 && v_stride_t % 8 == 0 && v_stride_h % 8 == 0 &&
-                     rope_stride_t % 8 == 0 && q_out_stride_t % 8 == 0 &&
-                     q_out_stride_h % 8 == 0 && pool_stride_slot % 8 == 0 &&
-                     pool_stride_head % 8 == 0,
+  // 16-byte vectors: every row start and every stride a multiple of 16 bytes
+  const int64_t ve = dtype == DSP_F32 ? 4 : 8;  // elements per 16 bytes
+  DSP_HOST_CHECK(q_stride_t % ve == 0 && q_stride_h % ve == 0 && k_stride_t % ve == 0 &&
+                     k_stride_h % ve == 0 && v_stride_t % ve == 0 && v_stride_h % ve == 0 &&
+                     rope_stride_t % ve == 0 && q_out_stride_t % ve == 0 &&
+                     q_out_stride_h % ve == 0 && pool_stride_slot % ve == 0 &&
+                     pool_stride_head % ve == 0,
                  DSP_EALIGN);
   DSP_HOST_CHECK(dsp_aligned(q, 16) && dsp_aligned(k, 16) && dsp_aligned(v, 16) &&
                      dsp_aligned(cos_table, 16) && dsp_aligned(sin_table, 16) &&
@@ -193,11 +276,22 @@ extern "C" int dsp_qk_norm_rope_append(
                      (q_norm_weight == nullptr ||
                       (dsp_aligned(q_norm_weight, 16) && dsp_aligned(k_norm_weight, 16))),
                  DSP_EALIGN);
-  const int rows_per_block = 4 * (64 / (D / 8));
+  const int rows_per_block = 4 * (64 / (D / int(ve)));
   const int64_t rows = T * int64_t(Hq + KVH);
   const int64_t grid = (rows + rows_per_block - 1) / rows_per_block;
   DSP_HOST_CHECK(grid < (int64_t(1) << 31), DSP_EINVAL);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == DSP_F32)
+    return launch_f32(D, static_cast<unsigned>(grid), s, static_cast<const float*>(q),
+                      q_stride_t, q_stride_h, static_cast<const float*>(k), k_stride_t,
+                      k_stride_h, static_cast<const float*>(v), v_stride_t, v_stride_h,
+                      static_cast<const float*>(q_norm_weight),
+                      static_cast<const float*>(k_norm_weight), eps,
+                      static_cast<const float*>(cos_table), static_cast<const float*>(sin_table),
+                      rope_stride_t, slots, T, Hq, KVH, static_cast<float*>(q_out),
+                      q_out_stride_t, q_out_stride_h, static_cast<float*>(k_pool),
+                      static_cast<float*>(v_pool), num_slots, pool_stride_slot,
+                      pool_stride_head, err_count);
   auto qh = static_cast<const uint16_t*>(q);
   auto kh = static_cast<const uint16_t*>(k);
   auto vh = static_cast<const uint16_t*>(v);

@@ -44,10 +44,10 @@ def qk_norm_rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: 
     if (q_norm is None) != (k_norm is None):
         raise ValueError("q_norm and k_norm come together")
     dt = q.dtype
-    if dt not in (torch.bfloat16, torch.float16) or k.dtype != dt or v.dtype != dt \
-            or cache.key.dtype != dt:
+    if dt not in (torch.bfloat16, torch.float16, torch.float32) or k.dtype != dt \
+            or v.dtype != dt or cache.key.dtype != dt:
         raise ValueError(f"q/k/v/cache dtypes {q.dtype}/{k.dtype}/{v.dtype}/{cache.key.dtype}: "
-                         "the prologue kernel takes bf16 or fp16, all the same")
+                         "the prologue kernel takes bf16, fp16 or fp32, all the same")
     for t in (q, k, v):
         if t.stride(2) != 1:
             raise ValueError("head_dim must be contiguous in q, k and v")

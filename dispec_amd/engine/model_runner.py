@@ -82,6 +82,9 @@ class ModelRunner:
         self.head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
         self.kv_groups = self.num_heads // self.num_kv_heads
         self.scale = self.head_dim ** -0.5
+        # the MFMA attention kernels (and with them the balanced verify split and the shared
+        # prefix) serve bf16 / fp16; fp32 models attend through the generic kernel
+        self._tuned_attention = self.dtype in (torch.bfloat16, torch.float16)
         attn0 = self.layers[0].self_attn
         self.qk_norm = hasattr(attn0, "q_norm") and hasattr(attn0, "k_norm")
         if "sliding_attention" in (getattr(cfg, "layer_types", None) or []):
@@ -163,7 +166,7 @@ class ModelRunner:
         heads, 5 queries: 44 against 93 us; similar lengths: fixed partitions 0-5 %
         faster)."""
         B = len(seq_meta)
-        if (max_q_len * self.kv_groups > 16 or B > 512 or bs < 16
+        if (max_q_len * self.kv_groups > 16 or B > 512 or bs < 16 or not self._tuned_attention
                 or self.head_dim not in (32, 64, 128)):
             return False
         P = _lib.lib().dsp_paged_mq_partition_tokens(B, self.num_heads, self.num_kv_heads,
@@ -176,7 +179,7 @@ class ModelRunner:
         sees, rounded down to a multiple of 128 -- or 0 when the batch is too small, the
         prefix too short, or the shape one the shared-prefix kernels do not serve."""
         B = len(seq_meta)
-        if (B < self.shared_prefix_min_seqs or B > 1024 or bs < 16
+        if (B < self.shared_prefix_min_seqs or B > 1024 or bs < 16 or not self._tuned_attention
                 or self.head_dim not in (64, 128)):
             return 0
         limit = min(m.ctx_len - m.q_len for m in seq_meta) // bs   # full blocks all queries see

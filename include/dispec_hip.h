@@ -363,8 +363,9 @@ int dsp_kv_rope(const void* x, int64_t x_layer_stride, void* y, int64_t y_layer_
  *                  err_count, that token's k/v not written).
  *   q_out        : [T, Hq, D] rotated q (may alias q when the strides match).
  *   k/v_pool     : one layer, [num_slots, KVH, D] with (slot, head) strides.
- * dtype DSP_BF16 / DSP_F16; D in {32, 64, 128, 256}; all strides multiples of 8 elements
- * and all pointers 16-byte aligned. */
+ * dtype DSP_BF16 / DSP_F16 / DSP_F32 (every tensor of that dtype; fp32 rounds nowhere but
+ * in its own arithmetic, as torch's fp32 ops do); D in {32, 64, 128, 256}; all strides
+ * multiples of 16 bytes and all pointers 16-byte aligned. */
 int dsp_qk_norm_rope_append(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                             const void* k, int64_t k_stride_t, int64_t k_stride_h,
                             const void* v, int64_t v_stride_t, int64_t v_stride_h,

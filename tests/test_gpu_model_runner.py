@@ -21,20 +21,20 @@ DEV = "cuda"
 FAMILIES = ("qwen3", "qwen2")
 
 
-def _pair(family):
-    base = toy_lm(family).to(torch.bfloat16)
-    ref = copy.deepcopy(base).float()          # same bf16-rounded weights, fp32 math
+def _pair(family, dtype=torch.bfloat16):
+    base = toy_lm(family).to(dtype)
+    ref = copy.deepcopy(base).float()          # same rounded weights, fp32 math
     return base.to(DEV), ref
 
 
 class _Both:
     """Drive the HIP runner and the CPU oracle through identical cache operations."""
 
-    def __init__(self, gpu_model, cpu_model, num_blocks=64, bs=16):
+    def __init__(self, gpu_model, cpu_model, num_blocks=64, bs=16, dtype=torch.bfloat16):
         from dispec_amd.engine.model_runner import ModelRunner
         from dispec_amd.kv.paged_cache import PagedKVCache
         self.runner = ModelRunner(gpu_model, attn_backend="hip")
-        self.cache = PagedKVCache.for_model(gpu_model.config, num_blocks, bs, torch.bfloat16, DEV)
+        self.cache = PagedKVCache.for_model(gpu_model.config, num_blocks, bs, dtype, DEV)
         cfg = cpu_model.config
         shape = (cfg.num_hidden_layers, num_blocks * bs, cfg.num_key_value_heads, cfg.head_dim)
         self.key, self.value = torch.zeros(shape), torch.zeros(shape)
@@ -84,6 +84,28 @@ def test_prefill_then_decode_matches_native(family):
         c = _cos(got[0], ref[0]).item()
         assert c >= 0.999, f"step {step}, ctx {cur + 1}: cosine {c:.5f}"
         nxt, cur = int(ref[0].argmax()), cur + 1
+
+
+@pytest.mark.parametrize("family", sorted(FAMILIES))
+def test_fp32_model_end_to_end(family):
+    """An fp32 model on the HIP path: the fp32 prologue and the generic attention kernel
+    (the MFMA kernels serve bf16 / fp16), against the oracle's fp32 native forward --
+    prefill, 20 decode steps and a chunked continuation; logits cosine >= 0.99999."""
+    gm, cm = _pair(family, torch.float32)
+    both = _Both(gm, cm, dtype=torch.float32)
+    assert not both.runner._tuned_attention
+    ids = torch.randint(0, 128, (37,), generator=torch.Generator().manual_seed(16)).tolist()
+    got, ref = both.forward([(1, ids, 0)])
+    assert _cos(got, ref).min() >= 0.99999
+    nxt, cur = int(ref[-1].argmax()), len(ids)
+    for step in range(20):
+        got, ref = both.forward([(1, [nxt], cur)])
+        c = _cos(got[0], ref[0]).item()
+        assert c >= 0.99999, f"fp32 step {step}: cosine {c:.7f}"
+        nxt, cur = int(ref[0].argmax()), cur + 1
+    more = torch.randint(0, 128, (9,), generator=torch.Generator().manual_seed(17)).tolist()
+    got, ref = both.forward([(1, more, cur)])
+    assert _cos(got, ref).min() >= 0.99999
 
 
 @pytest.mark.parametrize("family", sorted(FAMILIES))

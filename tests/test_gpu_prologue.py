@@ -155,3 +155,41 @@ def test_prologue_rejects_bad_arguments(hip):
         qk_norm_rope_append(d(q), d(k), d(v), d(cos[:3]), d(sin[:3]), d(slots), cache, 0)
     with pytest.raises(RuntimeError):  # CPU tensors: no CPU path
         qk_norm_rope_append(q, k, v, cos, sin, slots, cache, 0)
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_prologue_fp32(hip, D):
+    """fp32 models: the same steps with fp32 rounding only (numpy float32, one rounding per
+    op as torch's fp32 ops); bound 4 fp32 ulp at the row's scale (the variance's summation
+    order and rsqrt's last bits), v rows and untouched pool rows bit-exact."""
+    from dispec_amd.engine.hip_prologue import qk_norm_rope_append
+    T, Hq, KVH = 9, 8, 2
+    dt = torch.float32
+    q, k, v, wq, wk, cos, sin, slots, cache, kp0, vp0 = _setup(T, Hq, KVH, D, dt, True, 95 + D)
+    out = qk_norm_rope_append(q.to(DEV), k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV),
+                              slots.to(DEV), cache, 0, _Norm(wq.to(DEV), 1e-6),
+                              _Norm(wk.to(DEV), 1e-6))
+    torch.cuda.synchronize()
+    f = np.float32
+
+    def norm(x, w):
+        var = np.mean(x * x, axis=-1, keepdims=True, dtype=f)
+        inv = (f(1) / np.sqrt(var + f(1e-6))).astype(f)
+        return (w * (x * inv)).astype(f)
+
+    c, s = cos.numpy()[:, None], sin.numpy()[:, None]
+
+    def rope(x):
+        h = x.shape[-1] // 2
+        rot = np.concatenate([-x[..., h:], x[..., :h]], -1)
+        return (x * c + rot * s).astype(f)
+    qo = rope(norm(q.numpy(), wq.numpy()))
+    ko = rope(norm(k.numpy(), wk.numpy()))
+    kp, vp = kp0.numpy().copy(), vp0.numpy().copy()
+    kp[slots.numpy()] = ko
+    vp[slots.numpy()] = v.numpy()
+    for got, want, what in ((out.cpu().numpy(), qo, "q"), (cache.key[0].cpu().numpy(), kp, "k")):
+        bound = 4 * 2.0 ** -23 * np.abs(want).max(axis=-1, keepdims=True)
+        worst = float((np.abs(got - want) - bound).max())
+        assert worst <= 0, f"{what} fp32 D={D}: {worst:.3g} beyond 4 row ulp"
+    assert np.array_equal(cache.value[0].cpu().numpy(), vp), "v pool"

@@ -11,7 +11,7 @@ from dispec_amd.engine.model_runner import ModelRunner, SeqMeta
 
 def _runner(head_dim=128):
     return SimpleNamespace(shared_prefix_min_seqs=4, shared_prefix_min_tokens=512,
-                           head_dim=head_dim)
+                           head_dim=head_dim, _tuned_attention=True)
 
 
 def _detect(tables, q_lens, ctx, bs=16, head_dim=128):
@@ -59,3 +59,13 @@ def test_not_used():
     tables[2][50] = 999                                        # diverges after 50 blocks
     assert _detect(tables, [5] * 6, [2100] * 6) == 768         # 50 blocks = 800 tokens
     assert _detect(_forks(6, 128, 2), [5] * 6, [2100] * 6, head_dim=32) == 0
+
+
+def test_fp32_models_do_not_take_the_shared_prefix():
+    """The shared-prefix kernel serves bf16 / fp16; an fp32 runner attends per sequence."""
+    tables = [list(range(130)) + [200 + i] for i in range(8)]
+    meta = [SeqMeta(t, 5, 2050 + 40 + 5) for t in tables]
+    table = torch.tensor(tables, dtype=torch.int32)
+    r = _runner()
+    r._tuned_attention = False
+    assert ModelRunner._shared_prefix(r, meta, table, 16) == 0

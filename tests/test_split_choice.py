@@ -21,7 +21,7 @@ def _built():
 
 def _prefer(ctx, q_len=5, Hq=16, KVH=8, D=128, bs=16):
     r = SimpleNamespace(num_heads=Hq, num_kv_heads=KVH, head_dim=D, kv_groups=Hq // KVH,
-                        balanced_key_fraction=0.6, _cus=256)
+                        balanced_key_fraction=0.6, _cus=256, _tuned_attention=True)
     meta = [SeqMeta([], q_len, c) for c in ctx]
     max_ctx = -(-max(ctx) // bs) * bs
     return ModelRunner._prefer_balanced(r, meta, q_len, max_ctx, bs)
