@@ -85,7 +85,8 @@ def _probe_lib():
                 "dsp_probe_slice_read": [P, P, c_int64, P, c_int64, c_int32, c_int32, c_int32,
                                          c_int32, c_int32, P, P],
                 "dsp_probe_gemm_fill": [P, c_int64, c_int64, c_int64, P, c_int64, c_int64,
-                                        c_int64, c_int32, P, P]}
+                                        c_int64, c_int32, P, P],
+                "dsp_probe_piece_scatter": [P, P, c_int64, c_int64, P, P]}
         for name, args in sigs.items():
             fn = getattr(lib, name)
             fn.restype, fn.argtypes = c_int, args
@@ -962,7 +963,9 @@ def bench_copy_ceiling(torch) -> dict:
     """The ceiling of the byte-moving kernels on this GPU: a 2 GiB streaming copy
     (dsp_probe_stream_copy, non-temporal loads and stores), best of three grid sizes --
     64, 16 and 4 KiB per workgroup, the last two one-shot workgroups -- read + write bytes
-    over time."""
+    over time; and the same copy with its destinations permuted in 32 KiB blocks and in
+    2 KiB rows (dsp_probe_piece_scatter), the write patterns of scatter / block copy and of
+    the append."""
     from dispec_amd import _lib
     lib = _probe_lib()
     n = 2 << 30
@@ -977,9 +980,24 @@ def bench_copy_ceiling(torch) -> dict:
                        "probe")
         t = _time_gpu(torch, f, 10)
         best = t if best is None else min(best, t)
+    res = {"copy_ceiling_GBps": 2 * n / best / 1e9}
+    # the same copy with its destinations permuted in 32 KiB blocks (the scatter's and the
+    # block copy's write pattern) and in 2 KiB rows (the append's); "inorder32k" is that
+    # kernel with the identity permutation, the control
+    g = torch.Generator(device="cuda").manual_seed(9)
+    for name, piece, rand in (("inorder32k", 32768, False), ("block32k", 32768, True),
+                              ("row2k", 2048, True)):
+        perm = (torch.randperm(n // piece, generator=g, device="cuda") if rand else
+                torch.arange(n // piece, device="cuda")).to(torch.int32)
+
+        def f():
+            _lib.check(lib.dsp_probe_piece_scatter(src.data_ptr(), dst.data_ptr(), n, piece,
+                                                   perm.data_ptr(), stream), "probe")
+        res[f"scatter_{name}_ceiling_GBps"] = 2 * n / _time_gpu(torch, f, 10) / 1e9
+        del perm
     del src, dst
     torch.cuda.empty_cache()
-    return {"copy_ceiling_GBps": 2 * n / best / 1e9}
+    return res
 
 
 def _traffic_per_launch(profile="decode_c3_traffic.md", key=""):

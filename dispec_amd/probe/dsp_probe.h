@@ -42,6 +42,12 @@ int dsp_probe_slice_read(const void* k_cache, const void* v_cache, int64_t num_s
 int dsp_probe_gemm_fill(const void* a, int64_t lda, int64_t M, int64_t a_batch_stride,
                         const void* bt, int64_t ldb, int64_t N, int64_t K, int32_t batch,
                         uint32_t* sink, dsp_stream_t stream);
+/*   dsp_probe_piece_scatter: copy `bytes` of src to dst in pieces of piece_bytes (a multiple
+ *     of 16 dividing bytes), piece i landing at dst + dst_index[i] * piece_bytes (the caller
+ *     gives a permutation, so every destination is written once): the ceiling of writes to
+ *     random 32 KiB blocks (scatter, block copy) or 2 KiB rows (append). */
+int dsp_probe_piece_scatter(const void* src, void* dst, int64_t bytes, int64_t piece_bytes,
+                            const int32_t* dst_index, dsp_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -96,6 +96,30 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(const dsp_u32x4* __res
   }
 }
 
+// A copy whose destinations follow a permutation: contiguous source pieces of piece_bytes
+// (a multiple of 16) go to dst + dst_index[i] * piece_bytes -- the write pattern of the
+// scatter (32 KiB blocks) and of the append (2 KiB rows) with no table or slot logic.  One
+// one-shot workgroup per 4 KiB of the source, one 16-byte vector per lane, non-temporal;
+// pieces of 4 KiB or more take one index per workgroup (a scalar load, as the transport
+// kernels read their block ids), smaller ones one per lane.  With the identity permutation
+// it is the same kernel writing in order, the control of the pattern's cost.
+__global__ __launch_bounds__(256) void piece_scatter_kernel(const dsp_u32x4* __restrict__ src,
+                                                            dsp_u32x4* __restrict__ dst,
+                                                            int64_t piece16, int64_t n16,
+                                                            const int32_t* __restrict__ dst_index) {
+  const int64_t base = int64_t(blockIdx.x) * 256;
+  const int64_t f = base + threadIdx.x;
+  if (piece16 >= 256) {
+    const int64_t i = base / piece16;          // uniform: the workgroup lies in one piece
+    const int64_t d = int64_t(dst_index[i]) * piece16 + (f - i * piece16);
+    if (f < n16) dsp_st_stream(dsp_ld_stream(src + f), dst + d);
+    return;
+  }
+  if (f >= n16) return;
+  const int64_t i = f / piece16;
+  dsp_st_stream(dsp_ld_stream(src + f), dst + int64_t(dst_index[i]) * piece16 + (f - i * piece16));
+}
+
 // The map GEMM's loads without its arithmetic: the same 256 x 256 tiles in the same
 // XCD-aware order, each 64-wide K stage of 256 A rows and 256 Bt rows (128 bytes each)
 // going straight into LDS with global_load_lds_dwordx4, two stages resident, one barrier
@@ -216,5 +240,23 @@ extern "C" int dsp_probe_gemm_fill(const void* a, int64_t lda, int64_t M, int64_
   gemm_fill_kernel<<<dim3(static_cast<unsigned>(tiles)), 512, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const uint16_t*>(a), lda, M, a_batch_stride, static_cast<const uint16_t*>(bt), ldb,
       N, K, sink);
+  return dsp_launch_status();
+}
+
+extern "C" int dsp_probe_piece_scatter(const void* src, void* dst, int64_t bytes,
+                                       int64_t piece_bytes, const int32_t* dst_index,
+                                       dsp_stream_t stream) {
+  DSP_HOST_CHECK(src && dst && dst_index && bytes >= 16 && piece_bytes >= 16, DSP_EINVAL);
+  DSP_HOST_CHECK(piece_bytes % 16 == 0 && bytes % piece_bytes == 0, DSP_EINVAL);
+  // a piece of 4 KiB or more must hold whole workgroups (4 KiB each)
+  DSP_HOST_CHECK(piece_bytes < 4096 || piece_bytes % 4096 == 0, DSP_EINVAL);
+  DSP_HOST_CHECK(dsp_aligned(src, 16) && dsp_aligned(dst, 16), DSP_EALIGN);
+  const int64_t n16 = bytes / 16;
+  const int64_t grid = (n16 + 255) / 256;
+  DSP_HOST_CHECK(grid < (int64_t(1) << 31), DSP_EINVAL);
+  piece_scatter_kernel<<<dim3(static_cast<unsigned>(grid)), 256, 0,
+                         static_cast<hipStream_t>(stream)>>>(
+      static_cast<const dsp_u32x4*>(src), static_cast<dsp_u32x4*>(dst), piece_bytes / 16, n16,
+      dst_index);
   return dsp_launch_status();
 }
