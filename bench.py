@@ -86,7 +86,8 @@ def _probe_lib():
                                          c_int32, c_int32, P, P],
                 "dsp_probe_gemm_fill": [P, c_int64, c_int64, c_int64, P, c_int64, c_int64,
                                         c_int64, c_int32, P, P],
-                "dsp_probe_piece_scatter": [P, P, c_int64, c_int64, P, P]}
+                "dsp_probe_piece_scatter": [P, P, c_int64, c_int64, P, P],
+                "dsp_probe_piece_fill": [P, c_int64, c_int64, P, P]}
         for name, args in sigs.items():
             fn = getattr(lib, name)
             fn.restype, fn.argtypes = c_int, args
@@ -614,10 +615,15 @@ def bench_c4(torch) -> dict:
     for s in range(S):
         _, p = mgr.cow_fork(owner, s)
         pairs += p
-    src = torch.tensor([p[0] for p in pairs], dtype=torch.int32, device=dev)
+    # every pair copies the prompt's one partial block: copy_blocks routes such a list to the
+    # fan-out copy (the id list already on the GPU here, as a captured step would have it)
+    assert len({p[0] for p in pairs}) == 1
     dst = torch.tensor([p[1] for p in pairs], dtype=torch.int32, device=dev)
-    cow_s = _time_gpu_cold(torch, lambda: cache.copy_blocks_device(cache, src, dst), 20)
-    cow_warm_s = _time_gpu(torch, lambda: cache.copy_blocks_device(cache, src, dst), 20)
+    fork_src = pairs[0][0]
+    cow_s = _time_gpu_cold(torch, lambda: cache.copy_block_fanout_device(cache, fork_src, dst),
+                           20)
+    cow_warm_s = _time_gpu(torch, lambda: cache.copy_block_fanout_device(cache, fork_src, dst),
+                           20)
     cow_bytes = 2 * 2 * L * len(pairs) * cache.block_bytes
     # suffix + draft tokens: one append per layer for all 32 sequences
     rows, wslots = [], []
@@ -965,7 +971,9 @@ def bench_copy_ceiling(torch) -> dict:
     64, 16 and 4 KiB per workgroup, the last two one-shot workgroups -- read + write bytes
     over time; and the same copy with its destinations permuted in 32 KiB blocks and in
     2 KiB rows (dsp_probe_piece_scatter), the write patterns of scatter / block copy and of
-    the append."""
+    the append; and stores alone, in order and to random 32 KiB blocks (dsp_probe_piece_fill,
+    bytes written over time: the copy-on-write fork reads its one source block from L2 and
+    only writes HBM)."""
     from dispec_amd import _lib
     lib = _probe_lib()
     n = 2 << 30
@@ -994,6 +1002,12 @@ def bench_copy_ceiling(torch) -> dict:
             _lib.check(lib.dsp_probe_piece_scatter(src.data_ptr(), dst.data_ptr(), n, piece,
                                                    perm.data_ptr(), stream), "probe")
         res[f"scatter_{name}_ceiling_GBps"] = 2 * n / _time_gpu(torch, f, 10) / 1e9
+        if piece == 32768:
+            # the same destinations written without reading anything: HBM write bandwidth
+            def fill():
+                _lib.check(lib.dsp_probe_piece_fill(dst.data_ptr(), n, piece, perm.data_ptr(),
+                                                    stream), "probe")
+            res[f"write_only_{name}_GBps"] = n / _time_gpu(torch, fill, 10) / 1e9
         del perm
     del src, dst
     torch.cuda.empty_cache()

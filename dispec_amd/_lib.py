@@ -36,6 +36,8 @@ SIGNATURES: dict[str, tuple] = {
                                     c_int64, _P, _P]),
     "dsp_kv_copy_blocks": (c_int, [_P, _P, c_int64, c_int64, _P, _P, c_int64, c_int64, c_int64,
                                    c_int64, _P, _P, c_int64, _P, _P]),
+    "dsp_kv_copy_block_fanout": (c_int, [_P, _P, c_int64, c_int64, _P, _P, c_int64, c_int64,
+                                         c_int64, c_int64, c_int32, _P, c_int64, _P, _P]),
     "dsp_kv_gather": (c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int32, _P, c_int64,
                               _P, c_int32, c_int64, _P, _P, _P, _P]),
     "dsp_kv_scatter": (c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int32, _P, c_int64,

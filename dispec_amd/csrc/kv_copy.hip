@@ -94,6 +94,49 @@ __global__ __launch_bounds__(kThreads) void copy_blocks_kernel(
   piece_copy<VEC>(src, dst, min(kPiece, block_bytes - off));
 }
 
+// grid = (ceil(num_dst / kFanOut) * pieces per block, num_layers, 2 planes): one 4 KiB
+// piece of the source block, copied to kFanOut destinations.  Each thread loads its
+// vectors of the piece once and stores them kFanOut times (the fork of one block into
+// many sequences reads the source once per kFanOut copies, not once per copy).  The
+// destination ids come in one round trip: lane i loads id i, every wave reads them back as
+// scalars; ids past num_dst or out of range store nothing (an out-of-range id is counted).
+constexpr int kFanOut = 8;
+template <int VEC>
+__global__ __launch_bounds__(kThreads) void fanout_block_kernel(
+    const char* __restrict__ src_k, const char* __restrict__ src_v, int64_t src_layer_stride,
+    char* __restrict__ dst_k, char* __restrict__ dst_v, int64_t dst_layer_stride,
+    int64_t dst_num_blocks, int64_t block_bytes, int64_t src_block,
+    const int32_t* __restrict__ dst_blocks, int64_t num_dst, int32_t pieces_per_block,
+    int32_t* __restrict__ err_count) {
+  using V = typename dsp_vec<VEC>::type;
+  constexpr int U = int(kPiece / (kThreads * VEC));
+  const int64_t g = blockIdx.x / pieces_per_block;
+  const int64_t off = (blockIdx.x % pieces_per_block) * kPiece;
+  const int64_t l = blockIdx.y;
+  const int64_t n = min(kPiece, block_bytes - off) / VEC;
+  const int64_t il = min(g * kFanOut + (threadIdx.x & (kFanOut - 1)), num_dst - 1);
+  const int32_t db_l = dst_blocks[il];
+  const V* src = reinterpret_cast<const V*>((blockIdx.z == 0 ? src_k : src_v) +
+                                            l * src_layer_stride + src_block * block_bytes + off);
+  char* dbase = (blockIdx.z == 0 ? dst_k : dst_v) + l * dst_layer_stride + off;
+  V buf[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) buf[u] = dsp_ld_stream(src + min(int64_t(threadIdx.x + u * kThreads), n - 1));
+#pragma unroll
+  for (int p = 0; p < kFanOut; ++p) {
+    const int64_t db = __builtin_amdgcn_readlane(db_l, p);
+    const bool in = g * kFanOut + p < num_dst;
+    const bool ok = db >= 0 && db < dst_num_blocks;
+    if (in && !ok && threadIdx.x == 0 && off == 0 && l == 0 && blockIdx.z == 0 && err_count)
+      atomicAdd(err_count, 1);
+    V* dst = reinterpret_cast<V*>(dbase + (in && ok ? db : 0) * block_bytes);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (in && ok && threadIdx.x + u * kThreads < n)
+        dsp_st_stream(buf[u], dst + threadIdx.x + u * kThreads);
+  }
+}
+
 // --------------------------------------------------------------------------- J5a/J5c
 // grid = (max blocks per sequence * pieces per block, num_layers, 2 * num_seqs).  Block j
 // of sequence b in layer l covers tokens [j*bs, min((j+1)*bs, T_b)): contiguous in the pool
@@ -288,6 +331,57 @@ extern "C" int dsp_kv_copy_blocks(const void* src_k_pool, const void* src_v_pool
     default: DSP_COPY(1); break;
   }
 #undef DSP_COPY
+  return dsp_launch_status();
+}
+
+extern "C" int dsp_kv_copy_block_fanout(const void* src_k_pool, const void* src_v_pool,
+                                        int64_t src_layer_stride_bytes, int64_t src_num_blocks,
+                                        void* dst_k_pool, void* dst_v_pool,
+                                        int64_t dst_layer_stride_bytes, int64_t dst_num_blocks,
+                                        int64_t num_layers, int64_t block_bytes,
+                                        int32_t src_block, const int32_t* dst_blocks,
+                                        int64_t num_dst, int32_t* err_count,
+                                        dsp_stream_t stream) {
+  DSP_HOST_CHECK(src_k_pool && src_v_pool && dst_k_pool && dst_v_pool, DSP_EINVAL);
+  DSP_HOST_CHECK(dst_blocks || num_dst == 0, DSP_EINVAL);
+  DSP_HOST_CHECK(num_layers > 0 && num_layers <= 65535 && src_num_blocks >= 0 &&
+                     dst_num_blocks >= 0 && block_bytes > 0 && num_dst >= 0 &&
+                     num_dst < (int64_t(1) << 31),
+                 DSP_EINVAL);
+  DSP_HOST_CHECK(src_layer_stride_bytes >= src_num_blocks * block_bytes &&
+                     dst_layer_stride_bytes >= dst_num_blocks * block_bytes,
+                 DSP_EINVAL);
+  if (num_dst == 0) return DSP_OK;
+  // the source id is a host value: checked here, not counted
+  DSP_HOST_CHECK(src_block >= 0 && src_block < src_num_blocks, DSP_EINVAL);
+  const int vec = dsp_vec_width({block_bytes, src_layer_stride_bytes, dst_layer_stride_bytes,
+                                 int64_t(reinterpret_cast<uintptr_t>(src_k_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(src_v_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(dst_k_pool)),
+                                 int64_t(reinterpret_cast<uintptr_t>(dst_v_pool))});
+  const int64_t ppb = (block_bytes + kPiece - 1) / kPiece;
+  const int64_t groups = (num_dst + kFanOut - 1) / kFanOut;
+  DSP_HOST_CHECK(groups * ppb < (int64_t(1) << 31), DSP_EINVAL);
+  dim3 grid(static_cast<unsigned>(groups * ppb), static_cast<unsigned>(num_layers), 2u);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const char* sk = static_cast<const char*>(src_k_pool);
+  const char* sv = static_cast<const char*>(src_v_pool);
+  char* dk = static_cast<char*>(dst_k_pool);
+  char* dv = static_cast<char*>(dst_v_pool);
+#define DSP_FAN(V)                                                                         \
+  fanout_block_kernel<V><<<grid, kThreads, 0, s>>>(sk, sv, src_layer_stride_bytes, dk, dv,  \
+                                                   dst_layer_stride_bytes, dst_num_blocks,  \
+                                                   block_bytes, src_block, dst_blocks,      \
+                                                   num_dst, static_cast<int32_t>(ppb),      \
+                                                   err_count)
+  switch (vec) {
+    case 16: DSP_FAN(16); break;
+    case 8: DSP_FAN(8); break;
+    case 4: DSP_FAN(4); break;
+    case 2: DSP_FAN(2); break;
+    default: DSP_FAN(1); break;
+  }
+#undef DSP_FAN
   return dsp_launch_status();
 }
 

@@ -269,6 +269,15 @@ class PagedKVCache:
             self.num_layers, self.block_bytes, src_ids.data_ptr(), dst_ids.data_ptr(),
             src_ids.numel(), self._err.data_ptr(), self._stream()), "dsp_kv_copy_blocks")
 
+    def copy_block_fanout_device(self, src: "PagedKVCache", src_block: int,
+                                 dst_ids: torch.Tensor) -> None:
+        """Block src_block of src copied into every block of dst_ids (int32, on the GPU)."""
+        _lib.check(_lib.lib().dsp_kv_copy_block_fanout(
+            src.key.data_ptr(), src.value.data_ptr(), src.layer_bytes, src.num_blocks,
+            self.key.data_ptr(), self.value.data_ptr(), self.layer_bytes, self.num_blocks,
+            self.num_layers, self.block_bytes, int(src_block), dst_ids.data_ptr(),
+            dst_ids.numel(), self._err.data_ptr(), self._stream()), "dsp_kv_copy_block_fanout")
+
     # -- block copies (copy-on-write, prefix-cache spill) ----------------------------------
     def copy_blocks_from(self, src: "PagedKVCache", src_ids: list[int], dst_ids: list[int]) -> None:
         """dst[l, block d] = src[l, block s] for every layer, K and V."""
@@ -280,6 +289,13 @@ class PagedKVCache:
             return
         if src is self and set(src_ids) & set(dst_ids):
             raise ValueError("a block is both copied from and written in one copy_blocks call")
+        if len(src_ids) > 1 and len(set(src_ids)) == 1 and 0 <= src_ids[0] < src.num_blocks:
+            # one block forked into many (copy-on-write children of one prompt): read it
+            # once per group of copies
+            dst = torch.tensor(list(dst_ids), dtype=torch.int32).to(self.key.device)
+            self.copy_block_fanout_device(src, src_ids[0], dst)
+            self._after()
+            return
         ids = torch.tensor([list(src_ids), list(dst_ids)], dtype=torch.int32).to(self.key.device)
         _lib.check(_lib.lib().dsp_kv_copy_blocks(
             src.key.data_ptr(), src.value.data_ptr(), src.layer_bytes, src.num_blocks,

@@ -48,6 +48,11 @@ int dsp_probe_gemm_fill(const void* a, int64_t lda, int64_t M, int64_t a_batch_s
  *     random 32 KiB blocks (scatter, block copy) or 2 KiB rows (append). */
 int dsp_probe_piece_scatter(const void* src, void* dst, int64_t bytes, int64_t piece_bytes,
                             const int32_t* dst_index, dsp_stream_t stream);
+/*   dsp_probe_piece_fill: stores only -- fill `bytes` of dst (pieces of piece_bytes, a
+ *     multiple of 4096 dividing bytes) with a constant, piece i at dst + dst_index[i] *
+ *     piece_bytes: HBM write bandwidth in order (identity) or to random 32 KiB blocks. */
+int dsp_probe_piece_fill(void* dst, int64_t bytes, int64_t piece_bytes, const int32_t* dst_index,
+                         dsp_stream_t stream);
 
 #ifdef __cplusplus
 }

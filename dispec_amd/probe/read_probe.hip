@@ -120,6 +120,21 @@ __global__ __launch_bounds__(256) void piece_scatter_kernel(const dsp_u32x4* __r
   dsp_st_stream(dsp_ld_stream(src + f), dst + int64_t(dst_index[i]) * piece16 + (f - i * piece16));
 }
 
+// Stores only: piece i of dst (piece_bytes, a multiple of 4096) filled with a constant at
+// dst + dst_index[i] * piece_bytes -- the write half of the copies above, alone (the
+// copy-on-write fork's 32 copies of one block read it from L2 and write HBM only).  One
+// one-shot workgroup per 4 KiB, one 16-byte non-temporal store per lane.
+__global__ __launch_bounds__(256) void piece_fill_kernel(dsp_u32x4* __restrict__ dst,
+                                                         int64_t piece16, int64_t n16,
+                                                         const int32_t* __restrict__ dst_index,
+                                                         uint32_t value) {
+  const int64_t base = int64_t(blockIdx.x) * 256;
+  const int64_t f = base + threadIdx.x;
+  const int64_t i = base / piece16;  // uniform: the workgroup lies in one piece
+  const int64_t d = int64_t(dst_index[i]) * piece16 + (f - i * piece16);
+  if (f < n16) dsp_st_stream(dsp_u32x4{value, value, value, value}, dst + d);
+}
+
 // The map GEMM's loads without its arithmetic: the same 256 x 256 tiles in the same
 // XCD-aware order, each 64-wide K stage of 256 A rows and 256 Bt rows (128 bytes each)
 // going straight into LDS with global_load_lds_dwordx4, two stages resident, one barrier
@@ -258,5 +273,20 @@ extern "C" int dsp_probe_piece_scatter(const void* src, void* dst, int64_t bytes
                          static_cast<hipStream_t>(stream)>>>(
       static_cast<const dsp_u32x4*>(src), static_cast<dsp_u32x4*>(dst), piece_bytes / 16, n16,
       dst_index);
+  return dsp_launch_status();
+}
+
+extern "C" int dsp_probe_piece_fill(void* dst, int64_t bytes, int64_t piece_bytes,
+                                    const int32_t* dst_index, dsp_stream_t stream) {
+  DSP_HOST_CHECK(dst && dst_index && bytes >= 4096 && piece_bytes >= 4096, DSP_EINVAL);
+  DSP_HOST_CHECK(piece_bytes % 4096 == 0 && bytes % piece_bytes == 0, DSP_EINVAL);
+  DSP_HOST_CHECK(dsp_aligned(dst, 16), DSP_EALIGN);
+  const int64_t n16 = bytes / 16;
+  const int64_t grid = n16 / 256;
+  DSP_HOST_CHECK(grid < (int64_t(1) << 31), DSP_EINVAL);
+  piece_fill_kernel<<<dim3(static_cast<unsigned>(grid)), 256, 0,
+                      static_cast<hipStream_t>(stream)>>>(static_cast<dsp_u32x4*>(dst),
+                                                          piece_bytes / 16, n16, dst_index,
+                                                          0x3f803f80u);
   return dsp_launch_status();
 }

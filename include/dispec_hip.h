@@ -100,6 +100,21 @@ int dsp_kv_copy_blocks(const void* src_k_pool, const void* src_v_pool,
                        const int32_t* src_blocks, const int32_t* dst_blocks,
                        int64_t num_pairs, int32_t* err_count, dsp_stream_t stream);
 
+/* J2 for one source block copied into many: the copy-on-write fork of one partial block
+ * into every child of a prompt (block_manager.py:119-126, one cow_fork per child).  Same
+ * result as dsp_kv_copy_blocks with every src_blocks[i] == src_block; the source is read
+ * once per 8 copies instead of once per copy.
+ *   src_block  : host value, must lie in [0, src_num_blocks) (else DSP_EINVAL).
+ *   dst_blocks : int32[num_dst] device array; an id outside [0, dst_num_blocks) is skipped
+ *                and counted in *err_count.  No destination may equal the source when the
+ *                pools are the same. */
+int dsp_kv_copy_block_fanout(const void* src_k_pool, const void* src_v_pool,
+                             int64_t src_layer_stride_bytes, int64_t src_num_blocks,
+                             void* dst_k_pool, void* dst_v_pool, int64_t dst_layer_stride_bytes,
+                             int64_t dst_num_blocks, int64_t num_layers, int64_t block_bytes,
+                             int32_t src_block, const int32_t* dst_blocks, int64_t num_dst,
+                             int32_t* err_count, dsp_stream_t stream);
+
 /* ------------------------------------------------------------------------ J5a / J5c
  * Block-table gather of whole sequences over every layer into contiguous transport
  * buffers, and the inverse scatter.

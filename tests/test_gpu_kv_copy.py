@@ -194,6 +194,58 @@ def test_copies_split_into_pieces(hip, bs, H, D, dtype):
     c.check_errors()
 
 
+@pytest.mark.parametrize("bs,H,D,dtype", [(16, 8, 128, torch.bfloat16),  # 32 KiB blocks
+                                          (32, 3, 40, torch.bfloat16),   # 7680 B: a part piece
+                                          (16, 3, 5, torch.float16),     # 30 B rows
+                                          (16, 1, 8, torch.float32)])    # 512 B blocks
+@pytest.mark.parametrize("n_dst", [2, 8, 13, 32])
+def test_fanout_copy_of_one_block(hip, bs, H, D, dtype, n_dst):
+    """copy_blocks with one source for every pair (the copy-on-write fork of one partial
+    block into many children) runs dsp_kv_copy_block_fanout: bit-exact against the same
+    pairs copied one by one, for group sizes around its 8 copies per workgroup."""
+    L, NB = 3, 48
+    c = _cache(L, NB, bs, H, D, dtype=dtype, seed=200 + n_dst + D)
+    kp, vp = bits(c.key), bits(c.value)
+    dst = torch.randperm(NB - 1, generator=gen(201 + n_dst))[:n_dst].add(1).tolist()
+    pairs = [(0, d) for d in dst]
+    c.copy_blocks(pairs)
+    ref_cpu.copy_blocks(kp, kp, pairs, bs)
+    ref_cpu.copy_blocks(vp, vp, pairs, bs)
+    assert np.array_equal(bits(c.key), kp) and np.array_equal(bits(c.value), vp)
+    c.check_errors()
+
+
+def test_fanout_into_a_second_pool_and_bad_ids(hip):
+    """One block of one pool into blocks of another (prefix-cache spill of a shared block);
+    destination ids outside the pool are skipped and counted, through the C-ABI."""
+    from dispec_amd import _lib
+    src = _cache(2, 8, 16, 2, 64, seed=210)
+    dst = _cache(2, 12, 16, 2, 64, seed=211)
+    kd, vd = bits(dst.key), bits(dst.value)
+    ids = [3, 12, 7, -1, 0, 11, 5, 9, 1, 2]            # 12 and -1 lie outside dst
+    d = torch.tensor(ids, dtype=torch.int32, device=DEV)
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    st = _lib.lib().dsp_kv_copy_block_fanout(
+        src.key.data_ptr(), src.value.data_ptr(), src.layer_bytes, src.num_blocks,
+        dst.key.data_ptr(), dst.value.data_ptr(), dst.layer_bytes, dst.num_blocks,
+        dst.num_layers, dst.block_bytes, 6, d.data_ptr(), len(ids), err.data_ptr(),
+        torch.cuda.current_stream().cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    good = [(6, i) for i in ids if 0 <= i < 12]
+    ref_cpu.copy_blocks(bits(src.key), kd, good, 16)
+    ref_cpu.copy_blocks(bits(src.value), vd, good, 16)
+    assert np.array_equal(bits(dst.key), kd) and np.array_equal(bits(dst.value), vd)
+    assert int(err.item()) == 2
+    # a source id outside the pool is a host-side argument error
+    st = _lib.lib().dsp_kv_copy_block_fanout(
+        src.key.data_ptr(), src.value.data_ptr(), src.layer_bytes, src.num_blocks,
+        dst.key.data_ptr(), dst.value.data_ptr(), dst.layer_bytes, dst.num_blocks,
+        dst.num_layers, dst.block_bytes, 8, d.data_ptr(), len(ids), err.data_ptr(),
+        torch.cuda.current_stream().cuda_stream)
+    assert st != 0
+
+
 def test_copy_blocks_out_of_range_is_reported(hip):
     from dispec_amd.kv.paged_cache import PagedKVCache
     c = _cache(2, 8, 16, 2, 64, seed=100)
