@@ -124,12 +124,18 @@ def check(status: int, what: str) -> None:
     raise RuntimeError(msg)
 
 
+_DTYPE_CODES: dict = {}
+
+
 def dtype_code(dtype) -> int:
-    import torch
-    codes = {torch.bfloat16: DSP_BF16, torch.float16: DSP_F16, torch.float32: DSP_F32}
-    if dtype not in codes:
+    if not _DTYPE_CODES:
+        import torch
+        _DTYPE_CODES.update({torch.bfloat16: DSP_BF16, torch.float16: DSP_F16,
+                             torch.float32: DSP_F32})
+    code = _DTYPE_CODES.get(dtype)
+    if code is None:
         raise ValueError(f"unsupported dtype {dtype}")
-    return codes[dtype]
+    return code
 
 
 def ptr(t) -> int | None:

@@ -36,6 +36,8 @@
 // (readlane), the second window loaded while the first is in use.
 #include <float.h>
 
+#include <atomic>
+
 #include "dsp_common.h"
 #include "dsp_internal.h"
 #include "dsp_mfma.h"
@@ -603,11 +605,19 @@ int launch_balanced(int D, A... args) {
 namespace dsp_detail {
 
 int device_cus() {
+  // a device property: queried once per device (a race only repeats the same query)
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
   int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       cus <= 0)
     return 256;
+  if (dev >= 0 && dev < kMaxDevices) cached[dev].store(cus, std::memory_order_relaxed);
   return cus;
 }
 

@@ -36,6 +36,7 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxPartition = 1024;
+constexpr int kOneRoundCtx = 512;  // automatic block-table decode: unsplit up to this context
 
 struct Bf16Tag {};
 struct F16Tag {};
@@ -468,8 +469,12 @@ size_t fixed_workspace_bytes(int32_t B, int32_t Hq, int32_t D, int32_t max_ctx, 
 extern "C" size_t dsp_paged_decode_workspace_bytes(int32_t B, int32_t Hq, int32_t KVH, int32_t D,
                                                    int32_t max_ctx, int32_t partition_tokens) {
   if (B <= 0 || Hq <= 0 || KVH <= 0 || Hq % KVH != 0 || D <= 0 || max_ctx <= 0 ||
-      partition_tokens < 0)
+      (partition_tokens < 0 && partition_tokens != DSP_SPLIT_BALANCED))
     return 0;
+  if (partition_tokens == DSP_SPLIT_BALANCED)
+    return dsp_detail::balanced_decode_applies(B, KVH, D, max_ctx, 16)
+               ? dsp_detail::balanced_workspace_bytes(B, KVH, Hq / KVH, D, max_ctx)
+               : 0;
   if (partition_tokens > 0) return fixed_workspace_bytes(B, Hq, D, max_ctx, partition_tokens);
   // automatic: enough for whichever split the launch picks (balanced on block tables,
   // fixed partitions on slot tables)
@@ -503,10 +508,11 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   DSP_HOST_CHECK(num_slots > 0 || B == 0 || max_ctx == 0, DSP_EINVAL);
   DSP_HOST_CHECK(kv_stride_slot >= 0 && kv_stride_head >= 0, DSP_EINVAL);
   DSP_HOST_CHECK(dtype == DSP_BF16 || dtype == DSP_F16 || dtype == DSP_F32, DSP_EUNSUPPORTED);
-  DSP_HOST_CHECK(partition_tokens >= 0, DSP_EINVAL);
+  DSP_HOST_CHECK(partition_tokens >= 0 || partition_tokens == DSP_SPLIT_BALANCED, DSP_EINVAL);
   const int G = Hq / KVH;
   const int step = wg_step_for(D);
   if (dtype == DSP_F32 || step == 0 || G > 8) {
+    DSP_HOST_CHECK(partition_tokens != DSP_SPLIT_BALANCED, DSP_EUNSUPPORTED);
     // fp32 caches, head dims outside {16, 32, 64, 128}, groups above 8: the generic kernel
     DSP_HOST_CHECK(dsp_detail::generic_head_dim(D), DSP_EUNSUPPORTED);
     if (B == 0) return DSP_OK;
@@ -558,7 +564,19 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   const uint16_t* vh = static_cast<const uint16_t*>(v_cache);
   uint16_t* oh = static_cast<uint16_t*>(out);
   const bool bm = block_table != nullptr;
-  if (bm && partition_tokens == 0 &&
+  // Automatic split on block tables.  A small launch -- contexts of at most kOneRoundCtx
+  // keys and one MFMA workgroup per (sequence, KV head) for at most two per CU -- runs
+  // unsplit on the multi-query kernel: one launch, no combine (config 1, a draft model's
+  // decode: 7.8 against 11.9 us on the balanced split and its combine, graph-captured).
+  // Otherwise the balanced split where it applies.
+  const bool one_round = bm && partition_tokens == 0 && D >= 32 && max_ctx > 0 &&
+                         max_ctx <= kOneRoundCtx &&
+                         int64_t(B) * KVH <= 2 * int64_t(dsp_detail::device_cus());
+  if (partition_tokens == DSP_SPLIT_BALANCED) {
+    DSP_HOST_CHECK(bm && dsp_detail::balanced_decode_applies(B, KVH, D, max_ctx, block_size),
+                   DSP_EUNSUPPORTED);
+  }
+  if (bm && (partition_tokens == DSP_SPLIT_BALANCED || (partition_tokens == 0 && !one_round)) &&
       dsp_detail::balanced_decode_applies(B, KVH, D, max_ctx, block_size)) {
     // block tables, automatic split: every wave takes an equal share of the keys
     const size_t need = dsp_detail::balanced_workspace_bytes(B, KVH, G, D, max_ctx);
@@ -572,6 +590,7 @@ extern "C" int dsp_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
                                        o_stride_h, dtype == DSP_F16, err_count, s);
   }
   int P = partition_tokens > 0 ? partition_tokens
+          : one_round          ? (max_ctx + 127) / 128 * 128
                                : dsp_paged_decode_partition_tokens(B, KVH, D, max_ctx);
   DSP_HOST_CHECK(P % step == 0 && P <= kMaxPartition, DSP_EINVAL);
   const int num_parts = max_ctx > 0 ? (max_ctx + P - 1) / P : 1;

@@ -15,11 +15,45 @@ dims 8 and 256, more than 8 query heads per KV head) run on a generic wave-per-r
 
 from __future__ import annotations
 
+import functools
+
 import torch
 
 from dispec_amd import _lib
 
 _DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+@functools.lru_cache(maxsize=256)
+def _decode_ws_bytes(B, Hq, KVH, D, max_ctx, P) -> int:
+    return _lib.lib().dsp_paged_decode_workspace_bytes(B, Hq, KVH, D, max_ctx, P)
+
+
+@functools.lru_cache(maxsize=256)
+def _mq_ws_bytes(B, Hq, KVH, D, max_q_len, max_ctx, P) -> int:
+    return _lib.lib().dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, max_q_len, max_ctx, P)
+
+
+# Split-K workspaces of calls that bring none, one per (device, stream): kernels on one
+# stream run in order, so consecutive calls can share it; it grows to the largest need.
+# Under graph capture a call allocates its own (from the graph's pool), so that no captured
+# graph keeps the address of a cached workspace that a later, larger call replaces.
+_WS: dict = {}
+
+
+def _workspace(need: int, device, stream: int) -> torch.Tensor:
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(need // 4 + 1, dtype=torch.float32, device=device)
+    key = (device, stream)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() * 4 < need:
+        ws = torch.empty(need // 4 + 1, dtype=torch.float32, device=device)
+        _WS[key] = ws
+    return ws
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.int32 and t.is_contiguous() else t.to(torch.int32).contiguous()
 
 
 def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
@@ -41,9 +75,8 @@ def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
     scale = scale or D ** -0.5
     if q.stride(2) != 1:
         q = q.contiguous()
-    ctx_lens = ctx_lens.to(torch.int32).contiguous()
-    table = slot_table if slot_table is not None else block_table
-    table = table.to(torch.int32).contiguous()
+    ctx_lens = _i32(ctx_lens)
+    table = _i32(slot_table if slot_table is not None else block_table)
     if max_ctx is None:
         max_ctx = table.shape[1] if slot_table is not None else table.shape[1] * block_size
     out = torch.empty_like(q) if out is None else out
@@ -51,9 +84,10 @@ def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
         raise ValueError("out must have q's shape and dtype with head_dim contiguous")
     L = _lib.lib()
     P = int(partition_tokens)  # 0: the library's automatic split
-    need = L.dsp_paged_decode_workspace_bytes(B, Hq, KVH, D, max_ctx, P)
+    stream = _lib.stream_of(q)
+    need = _decode_ws_bytes(B, Hq, KVH, D, int(max_ctx), P)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
+        workspace = _workspace(need, q.device, stream)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     by_block = slot_table is None
     _lib.check(L.dsp_paged_decode(
@@ -63,8 +97,7 @@ def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
         block_size, None if by_block else table.data_ptr(),
         0 if by_block else table.stride(0), ctx_lens.data_ptr(), B, Hq, KVH, D,
         float(scale), int(max_ctx), int(P), _lib.ptr(workspace), ws_bytes, out.data_ptr(),
-        out.stride(0), out.stride(1), _lib.dtype_code(q.dtype), _lib.ptr(err),
-        _lib.stream_of(q)),
+        out.stride(0), out.stride(1), _lib.dtype_code(q.dtype), _lib.ptr(err), stream),
         "dsp_paged_decode")
     return out
 
@@ -180,9 +213,9 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
     scale = scale or D ** -0.5
     if q.stride(2) != 1:
         q = q.contiguous()
-    cu_q = cu_q.to(torch.int32).contiguous()
-    ctx_lens = ctx_lens.to(torch.int32).contiguous()
-    block_table = block_table.to(torch.int32).contiguous()
+    cu_q = _i32(cu_q)
+    ctx_lens = _i32(ctx_lens)
+    block_table = _i32(block_table)
     B = ctx_lens.numel()
     if cu_q.numel() != B + 1:
         raise ValueError(f"cu_q has {cu_q.numel()} entries for {B} sequences")
@@ -204,16 +237,17 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
         P = _lib.DSP_SPLIT_BALANCED
     else:
         P = int(partition_tokens)   # 0: the library picks the partition
-    need = L.dsp_paged_mq_workspace_bytes(B, Hq, KVH, D, int(max_q_len), int(max_ctx), P)
+    stream = _lib.stream_of(q)
+    need = _mq_ws_bytes(B, Hq, KVH, D, int(max_q_len), int(max_ctx), P)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need // 4 + 1, dtype=torch.float32, device=q.device)
+        workspace = _workspace(need, q.device, stream)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     head = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), S,
             k_cache.stride(0), k_cache.stride(1), block_table.data_ptr(), block_table.stride(0),
             block_size, cu_q.data_ptr(), ctx_lens.data_ptr(), B, Hq, KVH, D, float(scale),
             int(max_q_len), int(max_ctx))
     tail = (_lib.ptr(workspace), ws_bytes, out.data_ptr(), out.stride(0), out.stride(1),
-            _lib.dtype_code(q.dtype), _lib.ptr(err), _lib.stream_of(q))
+            _lib.dtype_code(q.dtype), _lib.ptr(err), stream)
     if sp:
         _lib.check(L.dsp_paged_mq_attention_shared_prefix(*head, sp, int(P), *tail),
                    "dsp_paged_mq_attention_shared_prefix")

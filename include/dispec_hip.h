@@ -160,12 +160,16 @@ int dsp_kv_scatter(void* k_pool, void* v_pool, int64_t num_layers,
  *   k/v_cache    : one layer, [num_slots, KVH, D] with strides (kv_stride_slot,
  *                  kv_stride_head), D contiguous; same strides for K and V.
  *   ctx_lens     : int32 [B], each in [0, max_ctx].  ctx_len 0 writes zeros.
- *   partition_tokens : 0 (automatic) or a split-K partition length.
- *                  0 with a block table, D in {32, 64, 128} and B <= 512: a balanced
- *                  split -- the launch's (sequence, KV head, 16-key unit) work is cut into
- *                  equal contiguous shares, one per wave, computed on the device from
- *                  ctx_lens -- and a log-sum-exp combine kernel.  Otherwise (or with a
- *                  slot table) fixed partitions of partition_tokens keys (0: chosen by
+ *   partition_tokens : 0 (automatic), DSP_SPLIT_BALANCED, or a split-K partition length.
+ *                  0 with a block table, D in {32, 64, 128}: max_ctx <= 512 with at most
+ *                  two (sequence, KV head) pairs per CU runs unsplit (one launch, no
+ *                  combine: such decodes are launch-bound); otherwise, for B <= 512, a
+ *                  balanced split -- the launch's (sequence, KV head, 16-key unit) work is
+ *                  cut into equal contiguous shares, one per wave, computed on the device
+ *                  from ctx_lens -- and a log-sum-exp combine kernel.  DSP_SPLIT_BALANCED
+ *                  asks for the balanced split whatever the size (block tables, D in {32,
+ *                  64, 128}, G <= 8, B <= 512; else DSP_EUNSUPPORTED).  Otherwise (or with
+ *                  a slot table) fixed partitions of partition_tokens keys (0: chosen by
  *                  dsp_paged_decode_partition_tokens) per (sequence, KV head), merged by
  *                  the combine kernel when a sequence spans more than one.  `workspace`
  *                  must hold dsp_paged_decode_workspace_bytes(..., partition_tokens)

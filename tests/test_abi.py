@@ -114,6 +114,10 @@ def test_partition_and_workspace_sizing(lib):
         (512 * 8 + 1024) * 4 * 130 * 4
     # a small launch: at least 4 units of 16 keys per wave -> 4*2*ceil(500/16)/4 = 64 waves
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, 0) == (4 * 2 + 64) * 7 * 66 * 4
+    # the balanced split asked for explicitly: its workspace alone
+    assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, _lib.DSP_SPLIT_BALANCED) == \
+        (4 * 2 + 64) * 7 * 66 * 4
+    assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, -2) == 0
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 3, 64, 500, 0) == 0     # 14 % 3 != 0
     # head_dim 256 (generic kernel): 1024-token partitions halved while the launch has fewer
     # than 1024 (sequence, KV head, partition) triples; one partition needs no workspace

@@ -38,8 +38,13 @@ def _slot_table(tables, lens, bs):
 
 
 def _run(lens, KVH, G, D, bs, seed, dtype=torch.bfloat16, extra_blocks=3, max_ctx=None,
-         partition_tokens=0):
+         partition_tokens=None):
+    """The balanced split by default (DSP_SPLIT_BALANCED: the automatic split runs small
+    launches unsplit instead)."""
+    from dispec_amd import _lib
     from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
+    if partition_tokens is None:
+        partition_tokens = _lib.DSP_SPLIT_BALANCED
     B = len(lens)
     NB = sum(-(-n // bs) for n in lens) + extra_blocks
     tables = random_block_tables(NB, lens, bs, seed)
@@ -159,7 +164,7 @@ def test_largest_batch_and_fallback(hip, B):
     """512 sequences is the largest batch the balanced split serves; 513 falls back to
     fixed partitions.  Both agree with the oracle."""
     lens = torch.randint(0, 200, (B,), generator=torch.Generator().manual_seed(B)).tolist()
-    out, ref = _run(lens, 2, 2, 64, 16, 1800 + B)
+    out, ref = _run(lens, 2, 2, 64, 16, 1800 + B, partition_tokens=0)
     assert_attention_close(f64(out), ref, f"B={B}")
 
 
@@ -180,7 +185,7 @@ def _raw_decode(q, kc, vc, bt, ctx, KVH, G, bs, max_ctx, err, P=0):
     return out
 
 
-@pytest.mark.parametrize("P", [0, 64])
+@pytest.mark.parametrize("P", [0, 64, -1])   # automatic, fixed, DSP_SPLIT_BALANCED
 def test_bad_lengths_are_clamped_and_counted(hip, P):
     KVH, G, D, bs = 2, 2, 64, 16
     kc, vc = randn((64, KVH, D), 1900).to(DEV), randn((64, KVH, D), 1901).to(DEV)
@@ -197,7 +202,7 @@ def test_bad_lengths_are_clamped_and_counted(hip, P):
     assert_attention_close(f64(out), ref, "clamped")
 
 
-@pytest.mark.parametrize("P", [0, 64])
+@pytest.mark.parametrize("P", [0, 64, -1])   # automatic, fixed, DSP_SPLIT_BALANCED
 def test_out_of_range_block_ids_are_counted_not_read(hip, P):
     KVH, G, D, bs = 2, 2, 64, 16
     kc, vc = randn((64, KVH, D), 2000).to(DEV), randn((64, KVH, D), 2001).to(DEV)
