@@ -112,6 +112,35 @@ def test_all_groups_and_head_dims(hip, D, G):
     assert_attention_close(f64(out), ref, f"D={D} G={G}")
 
 
+@pytest.mark.parametrize("B,max_ctx", [(256, 512),    # one round, unsplit: the largest
+                                       (257, 512),    # one pair past 2 per CU: balanced
+                                       (6, 513)])     # one key past 512: balanced
+def test_automatic_split_boundaries(hip, B, max_ctx):
+    """The automatic split of a block-table decode runs a small launch (max_ctx <= 512, at
+    most two (sequence, KV head) pairs per CU) unsplit in one launch and everything else on
+    the balanced split: both sides of each boundary agree with the oracle, with contexts
+    of 0 and of max_ctx among them."""
+    from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
+    KVH, G, D, bs = 2, 7, 64, 16
+    lens = torch.randint(1, max_ctx + 1, (B,), generator=gen(900 + B)).tolist()
+    lens[0], lens[-1] = 0, max_ctx
+    NB = sum(-(-n // bs) for n in lens) + 5
+    tables = random_block_tables(NB, lens, bs, 901 + B)
+    kc, vc = randn((NB * bs, KVH, D), 902 + B), randn((NB * bs, KVH, D), 903 + B)
+    q = randn((B, KVH * G, D), 904 + B)
+    width = -(-max_ctx // bs)
+    bt = torch.zeros((B, width), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    out = paged_decode_attention_blocks(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV),
+                                        torch.tensor(lens, dtype=torch.int32).to(DEV), G,
+                                        max_ctx=max_ctx)
+    st = _slot_table(tables, lens, bs, max_ctx)
+    ref = ref_cpu.decode_attention(f64(q), f64(kc), f64(vc), st.numpy(), lens, G)
+    assert_attention_close(f64(out), ref, f"B={B} max_ctx={max_ctx}")
+    assert not out[0].any()
+
+
 @pytest.mark.parametrize("P", [64, 128, 512, 1024])
 def test_split_k_partitions_agree(hip, P):
     """A 3000-token context split into P-token partitions and merged by the LSE combine."""
