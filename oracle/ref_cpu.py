@@ -131,11 +131,12 @@ def decode_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, sl
         slots = np.asarray(slot_table[b][:n], dtype=np.int64)
         k = np.repeat(np.asarray(k_cache[slots], dtype=np.float64), kv_groups, axis=1)  # (n,Hq,D)
         v = np.repeat(np.asarray(v_cache[slots], dtype=np.float64), kv_groups, axis=1)
-        s = np.einsum("hd,nhd->hn", q[b], k) * scale
+        # per head: s = q . K^T, o = softmax(s) . V (batched matmuls over the heads)
+        s = np.matmul(k.transpose(1, 0, 2), q[b][:, :, None])[:, :, 0] * scale  # (Hq, n)
         s -= s.max(axis=1, keepdims=True)
         p = np.exp(s)
         p /= p.sum(axis=1, keepdims=True)
-        out[b] = np.einsum("hn,nhd->hd", p, v)
+        out[b] = np.matmul(p[:, None, :], v.transpose(1, 0, 2))[:, 0, :]
     return out
 
 
@@ -164,12 +165,13 @@ def mq_attention(q: np.ndarray, k_cache: np.ndarray, v_cache: np.ndarray, slot_l
         n = slots.size
         k = np.repeat(np.asarray(k_cache[slots], dtype=np.float64), kv_groups, axis=1)
         v = np.repeat(np.asarray(v_cache[slots], dtype=np.float64), kv_groups, axis=1)
-        s = np.einsum("qhd,nhd->hqn", q[off:off + ql], k) * scale
+        # per head: s = Q . K^T (Hq, q_len, n), masked, softmax, o = P . V
+        s = np.matmul(q[off:off + ql].transpose(1, 0, 2), k.transpose(1, 2, 0)) * scale
         s = np.where(causal_lower_right_mask(ql, n)[None], s, -np.inf)
         s -= s.max(axis=2, keepdims=True)
         p = np.exp(s)
         p /= p.sum(axis=2, keepdims=True)
-        out[off:off + ql] = np.einsum("hqn,nhd->qhd", p, v)
+        out[off:off + ql] = np.matmul(p, v.transpose(1, 0, 2)).transpose(1, 0, 2)
         off += ql
     return out
 
