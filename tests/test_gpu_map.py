@@ -84,16 +84,15 @@ def _cfg(n_layers, heads, head_dim):
                            vocab_size=100, _name_or_path="org/m")
 
 
-@pytest.mark.parametrize("L_src,L_tgt,H,D,T,k", [(3, 4, 2, 4, 5, 2), (4, 3, 2, 64, 37, 2),
-                                                  (3, 2, 8, 128, 300, 1)])
-def test_map_matches_bf16_oracle_with_rope(L_src, L_tgt, H, D, T, k):
+def _check_map(L_src, L_tgt, H, D, T, k, seed):
+    """CrossModelKVMap.map with RoPE strip / re-apply against the oracle's bf16 chain."""
     from dispec_amd.kv.transfer import CrossModelKVMap
     kv = H * D
-    maps_k = _maps(L_src, L_tgt, kv, k, 100 + D, scale=kv ** -0.5)
-    maps_v = _maps(L_src, L_tgt, kv, k, 200 + D, scale=kv ** -0.5)
+    maps_k = _maps(L_src, L_tgt, kv, k, 100 + seed, scale=kv ** -0.5)
+    maps_v = _maps(L_src, L_tgt, kv, k, 200 + seed, scale=kv ** -0.5)
     kmap = CrossModelKVMap(_to_layer_maps(maps_k), _to_layer_maps(maps_v), _cfg(L_src, H, D),
                            _cfg(L_tgt, H, D))
-    kk, vv = randn((L_src, T, H, D), 1 + D), randn((L_src, T, H, D), 2 + D)
+    kk, vv = randn((L_src, T, H, D), 1 + seed), randn((L_src, T, H, D), 2 + seed)
     src_rope = ref_cpu.rope_tables(np.arange(T), D, 1e6)
     tgt_rope = ref_cpu.rope_tables(np.arange(T), D, 5e5)
     t = lambda a: torch.from_numpy(a).to(DEV)  # noqa: E731
@@ -109,6 +108,30 @@ def test_map_matches_bf16_oracle_with_rope(L_src, L_tgt, H, D, T, k):
     kb = _rotated_bound(_affine_bound(content, _np_maps(maps_k), T, H, D),
                         _affine_magnitude(content, _np_maps(maps_k), T, H, D), *tgt_rope)
     assert_bf16_within(bits(got_k), ref_k, kb, "keys")
+
+
+@pytest.mark.parametrize("L_src,L_tgt,H,D,T,k", [(3, 4, 2, 4, 5, 2), (4, 3, 2, 64, 37, 2),
+                                                  (3, 2, 8, 128, 300, 1)])
+def test_map_matches_bf16_oracle_with_rope(L_src, L_tgt, H, D, T, k):
+    _check_map(L_src, L_tgt, H, D, T, k, D)
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_map_random_shapes(case):
+    """Seeded random geometries: layer counts, heads, head dims (RoPE halves of 2..64),
+    token counts across the tile edges, 1-3 source layers per target row; the last cases
+    are large enough for the 256 x 256 direct-to-LDS kernel (>= 128 tiles)."""
+    r = np.random.default_rng(9000 + case)
+    if case >= 10:
+        H, D, T, k = 8, 128, (8192, 8448)[case - 10], 1
+        L_src, L_tgt = 1, 1
+    else:
+        H = int(r.choice([1, 2, 4, 8]))
+        D = int(r.choice([4, 8, 32, 64, 128]))
+        T = int(r.integers(1, 700))
+        k = int(r.integers(1, 4))
+        L_src, L_tgt = int(r.integers(k, 6)), int(r.integers(1, 6))
+    _check_map(L_src, L_tgt, H, D, T, k, 900 + case)
 
 
 def test_config5_shape_layer_selection():
