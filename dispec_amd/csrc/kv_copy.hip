@@ -9,10 +9,20 @@ namespace {
 
 constexpr int kThreads = 256;
 
+// Where the append kernel's stores of a row with an out-of-range slot go (their values are
+// never read): one 4 KiB region per device, shared by every launch.
+constexpr int kDroppedBytes = 4096;
+__device__ __attribute__((aligned(16))) char g_dropped_rows[kDroppedBytes];
+
 // ------------------------------------------------------------------------------- J1
 // One group of `lanes_per_row` lanes per token row; blockIdx.y selects K (0) or V (1).
 // kScatter: dense rows -> pool slots (append); otherwise pool slots -> dense rows.
-template <int VEC, bool kScatter>
+// The append's lane groups take R rows each (rows g, g + rows_per_wg, ...): R = 2 for
+// launches of up to kSmallAppend rows, 1 above.  Same-box A/B (cold cache, 2 KiB rows):
+// 8781 rows 4.0 TB/s at R 1, 4.3 at R 2, 4.2 at R 4, 4.05 at R 8; 32768 rows 5.1-5.2 at
+// R 1, 5.0 at R 2 and 4.
+constexpr int64_t kSmallAppend = 16384;
+template <int VEC, bool kScatter, int R>
 __global__ __launch_bounds__(kThreads) void slot_rows_kernel(
     char* __restrict__ k_pool, char* __restrict__ v_pool, int64_t num_slots,
     int64_t pool_stride, const char* __restrict__ k, const char* __restrict__ v,
@@ -20,21 +30,63 @@ __global__ __launch_bounds__(kThreads) void slot_rows_kernel(
     int32_t chunks_per_row, int32_t lanes_per_row, int32_t rows_per_wg,
     int32_t* __restrict__ err_count) {
   using V = typename dsp_vec<VEC>::type;
+  const int lane = threadIdx.x % lanes_per_row;
+  const char* plane_src = blockIdx.y == 0 ? k : v;
+  char* plane_pool = blockIdx.y == 0 ? k_pool : v_pool;
+  if constexpr (kScatter) {
+    // The dense source rows do not depend on the slots: each lane's first vector of its
+    // R rows is loaded together with the rows' slot indices, so the launch pays
+    // one memory round trip before its stores.  No branch on a slot lies between those
+    // loads and their stores (the compiler would sink the loads below it): a row with a bad
+    // slot, a row past the end and a lane past a row's end store into g_dropped_rows
+    // instead; bad rows are counted after the stores.
+    const int64_t row0 =
+        int64_t(blockIdx.x) * rows_per_wg * R + threadIdx.x / lanes_per_row;
+    const int c = lane;
+    V first[R];
+    int64_t slot[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int64_t row = min(row0 + int64_t(i) * rows_per_wg, num_tokens - 1);
+      first[i] = dsp_ld_stream(reinterpret_cast<const V*>(plane_src + row * src_stride) +
+                               min(c, chunks_per_row - 1));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // issued before the slot loads, not after their wait
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      slot[i] = slots[min(row0 + int64_t(i) * rows_per_wg, num_tokens - 1)];
+    V* const drop = reinterpret_cast<V*>(g_dropped_rows);
+    constexpr int kDropMask = kDroppedBytes / VEC - 1;
+    int bad = 0;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int64_t row = row0 + int64_t(i) * rows_per_wg;
+      const bool live = row < num_tokens;
+      const bool ok = live && slot[i] >= 0 && slot[i] < num_slots;
+      bad += live && !ok;
+      V* pooled = reinterpret_cast<V*>(plane_pool + (ok ? slot[i] : 0) * pool_stride);
+      dsp_st_stream(first[i], ok && c < chunks_per_row ? pooled + c : drop + (c & kDropMask));
+      if (ok) {  // rows longer than the lane group: the rest, one vector per lane at a time
+        const V* src = reinterpret_cast<const V*>(plane_src + row * src_stride);
+        for (int cc = c + lanes_per_row; cc < chunks_per_row; cc += lanes_per_row)
+          dsp_st_stream(dsp_ld_stream(src + cc), pooled + cc);
+      }
+    }
+    if (bad && lane == 0 && blockIdx.y == 0 && err_count) atomicAdd(err_count, bad);
+    return;
+  }
   const int64_t row = int64_t(blockIdx.x) * rows_per_wg + threadIdx.x / lanes_per_row;
   if (row >= num_tokens) return;
-  const int lane = threadIdx.x % lanes_per_row;
   const int64_t slot = slots[row];
   if (slot < 0 || slot >= num_slots) {
     if (lane == 0 && blockIdx.y == 0 && err_count) atomicAdd(err_count, 1);
     return;
   }
-  char* dense = const_cast<char*>(blockIdx.y == 0 ? k : v) + row * src_stride;
-  char* pooled = (blockIdx.y == 0 ? k_pool : v_pool) + slot * pool_stride;
-  const V* src = reinterpret_cast<const V*>(kScatter ? dense : pooled);
-  V* dst = reinterpret_cast<V*>(kScatter ? pooled : dense);
+  const V* src = reinterpret_cast<const V*>(plane_pool + slot * pool_stride);
+  V* dst = reinterpret_cast<V*>(const_cast<char*>(plane_src) + row * src_stride);
+  // Full rounds: U vectors per lane, all loads issued before the stores.
   constexpr int U = 4;
   int c = lane;
-  // Full rounds: U vectors per lane, all loads issued before the stores.
   for (; c + (U - 1) * lanes_per_row < chunks_per_row; c += U * lanes_per_row) {
     V buf[U];
 #pragma unroll
@@ -242,7 +294,8 @@ int launch_slot_rows(void* k_pool, void* v_pool, int64_t num_slots, int64_t pool
   int lanes = 1;
   while (lanes < chunks && lanes < kThreads) lanes <<= 1;
   const int rows_per_wg = kThreads / lanes;
-  const int64_t nwg = (num_tokens + rows_per_wg - 1) / rows_per_wg;
+  const int R = kScatter && num_tokens <= kSmallAppend ? 2 : 1;
+  const int64_t nwg = (num_tokens + int64_t(rows_per_wg) * R - 1) / (int64_t(rows_per_wg) * R);
   DSP_HOST_CHECK(nwg < (int64_t(1) << 31), DSP_EINVAL);
   dim3 grid(static_cast<unsigned>(nwg), 2u, 1u);
   char* kp = static_cast<char*>(k_pool);
@@ -250,9 +303,14 @@ int launch_slot_rows(void* k_pool, void* v_pool, int64_t num_slots, int64_t pool
   const char* kd = static_cast<const char*>(k);
   const char* vd = static_cast<const char*>(v);
 #define DSP_ROWS(V)                                                                          \
-  slot_rows_kernel<V, kScatter><<<grid, kThreads, 0, s>>>(                                   \
-      kp, vp, num_slots, pool_stride, kd, vd, dense_stride, slots, num_tokens,               \
-      static_cast<int32_t>(chunks), lanes, rows_per_wg, err_count)
+  if (R == 2)                                                                                \
+    slot_rows_kernel<V, kScatter, 2><<<grid, kThreads, 0, s>>>(                              \
+        kp, vp, num_slots, pool_stride, kd, vd, dense_stride, slots, num_tokens,             \
+        static_cast<int32_t>(chunks), lanes, rows_per_wg, err_count);                        \
+  else                                                                                       \
+    slot_rows_kernel<V, kScatter, 1><<<grid, kThreads, 0, s>>>(                              \
+        kp, vp, num_slots, pool_stride, kd, vd, dense_stride, slots, num_tokens,             \
+        static_cast<int32_t>(chunks), lanes, rows_per_wg, err_count)
   switch (vec) {
     case 16: DSP_ROWS(16); break;
     case 8: DSP_ROWS(8); break;

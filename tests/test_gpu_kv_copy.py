@@ -27,8 +27,9 @@ def _cache(L, NB, bs, H, D, dtype=torch.bfloat16, seed=0):
 
 @pytest.mark.parametrize("H,D,dtype", [(2, 64, torch.bfloat16), (8, 128, torch.bfloat16),
                                        (2, 4, torch.float32), (3, 5, torch.float16),
-                                       (2, 16, torch.float32)])
+                                       (2, 16, torch.float32), (16, 256, torch.bfloat16)])
 def test_append_bit_exact(hip, H, D, dtype):
+    # (16, 256): 8 KiB rows, more 16-byte vectors than a row's 256 lanes
     c = _cache(3, 40, 16, H, D, dtype, seed=10)
     kref, vref = bits(c.key), bits(c.value)
     T = 37
@@ -57,18 +58,40 @@ def test_append_from_strided_qkv_view(hip):
     assert np.array_equal(bits(c.key), kref) and np.array_equal(bits(c.value), vref)
 
 
-def test_append_out_of_range_slot_is_skipped_and_reported(hip):
-    c = _cache(1, 4, 16, 2, 64, seed=30)
-    before_k = bits(c.key)
+@pytest.mark.parametrize("H,D", [(2, 64), (16, 256)])
+def test_append_out_of_range_slot_is_skipped_and_reported(hip, H, D):
+    c = _cache(1, 4, 16, H, D, seed=30)
+    before_k, before_v = bits(c.key), bits(c.value)
     slots = torch.tensor([1, 64, 2, -1])                 # 64 == num_slots: out of range
-    k, v = randn((4, 2, 64), 31), randn((4, 2, 64), 32)
+    k, v = randn((4, H, D), 31), randn((4, H, D), 32)
     c.write(0, slots.to(DEV), k.to(DEV), v.to(DEV))
-    expect = before_k.copy()
-    expect[0, 1], expect[0, 2] = bits(k)[0], bits(k)[2]
-    assert np.array_equal(bits(c.key), expect)
+    expect_k, expect_v = before_k.copy(), before_v.copy()
+    expect_k[0, 1], expect_k[0, 2] = bits(k)[0], bits(k)[2]
+    expect_v[0, 1], expect_v[0, 2] = bits(v)[0], bits(v)[2]
+    assert np.array_equal(bits(c.key), expect_k) and np.array_equal(bits(c.value), expect_v)
     with pytest.raises(IndexError, match="2 out-of-range"):
         c.check_errors()
     c.check_errors()  # counter was reset
+
+
+@pytest.mark.parametrize("T", [16384, 16385, 20001])
+def test_append_around_the_small_launch_bound(hip, T):
+    """Up to 16384 rows the append's lane groups take two rows each, above it one: both
+    sides of the bound, with out-of-range slots among the rows and an odd row count."""
+    c = _cache(1, 1400, 16, 2, 64, seed=50)
+    kref, vref = bits(c.key), bits(c.value)
+    slots = torch.randperm(c.num_slots, generator=gen(51))[:T]
+    bad = torch.tensor([0, T // 2, T - 1])
+    slots[bad] = torch.tensor([-5, c.num_slots, c.num_slots + 100])
+    k, v = randn((T, 2, 64), 52), randn((T, 2, 64), 53)
+    c.write(0, slots.to(DEV), k.to(DEV), v.to(DEV))
+    good = np.ones(T, bool)
+    good[bad.numpy()] = False
+    ref_cpu.append(kref[0], slots.numpy()[good], bits(k)[good])
+    ref_cpu.append(vref[0], slots.numpy()[good], bits(v)[good])
+    assert np.array_equal(bits(c.key), kref) and np.array_equal(bits(c.value), vref)
+    with pytest.raises(IndexError, match="3 out-of-range"):
+        c.check_errors()
 
 
 def test_gather_slots_bit_exact(hip):
