@@ -206,15 +206,16 @@ __global__ __launch_bounds__(kThreads) void transport_kernel(
   const int64_t l = blockIdx.y;
   const int b = blockIdx.z >> 1;
   const int plane = blockIdx.z & 1;
+  // The block id does not depend on the lengths (j < bt_stride: the launch covers at most
+  // ceil(max_seqlen / bs) blocks per sequence): it is loaded beside them, and one branch
+  // tests both, so the copy starts one memory round trip after the workgroup does.
+  const int64_t blk = block_tables[int64_t(b) * bt_stride + j];
   const int64_t t0 = cu_seqlens[b];
   const int64_t T = cu_seqlens[b + 1] - t0;
   const int64_t first = j << log2_bs;
-  if (first >= T) return;
-  const int64_t seg = min(int64_t(1) << log2_bs, T - first) * row_bytes;
-  if (off >= seg) return;
-  const int64_t blk = block_tables[int64_t(b) * bt_stride + j];
-  if (blk < 0 || blk >= num_blocks) {
-    if (threadIdx.x == 0 && off == 0 && l == 0 && plane == 0 && err_count)
+  const int64_t seg = first < T ? min(int64_t(1) << log2_bs, T - first) * row_bytes : 0;
+  if (off >= seg || blk < 0 || blk >= num_blocks) {
+    if (off < seg && threadIdx.x == 0 && off == 0 && l == 0 && plane == 0 && err_count)
       atomicAdd(err_count, 1);
     return;
   }
