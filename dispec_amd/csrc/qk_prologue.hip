@@ -19,6 +19,10 @@
 
 namespace {
 
+// Where the prologue's stores with nowhere to go land (their values are never read): 16
+// bytes per thread of a 256-thread workgroup, one region per device shared by every launch.
+__device__ __attribute__((aligned(16))) uint16_t g_prologue_drop[256 * 8];
+
 struct Bf16Tag {};
 struct F16Tag {};
 
@@ -72,9 +76,22 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(
   const bool is_q = j < Hq;
   const int kh = j - Hq;
 
+  // Every load of the lane is issued here, together: the row, the norm weight, the RoPE
+  // cos/sin, the token's slot and the v row a k lane stores (a lane past the rows reads
+  // token 0's; q lanes read KV head 0's v row, lines the k lanes read anyway), so the lane
+  // waits for one memory round trip instead of one per dependent step.
   const uint16_t* src = is_q ? q + t * qst + int64_t(j) * qsh : k + t * kst + int64_t(kh) * ksh;
-  dsp_u32x4 x = live ? *reinterpret_cast<const dsp_u32x4*>(src + 8 * sub)
-                     : dsp_u32x4{0u, 0u, 0u, 0u};
+  const uint16_t* w = is_q ? qw : kw;
+  const dsp_u32x4 x = *reinterpret_cast<const dsp_u32x4*>(src + 8 * sub);
+  const dsp_u32x4 wv = *reinterpret_cast<const dsp_u32x4*>((w != nullptr ? w : src) + 8 * sub);
+  const dsp_u32x4 cv = *reinterpret_cast<const dsp_u32x4*>(cosp + t * rst + 8 * sub);
+  const dsp_u32x4 sv = *reinterpret_cast<const dsp_u32x4*>(sinp + t * rst + 8 * sub);
+  const int64_t slot = slots[t];
+  const dsp_u32x4 vrow = *reinterpret_cast<const dsp_u32x4*>(
+      v + t * vst + int64_t(is_q ? 0 : kh) * vsh + 8 * sub);
+  // a compiler-only fence (no instruction): the loads above are not moved below it
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_sched_barrier(0);
   float f[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -83,20 +100,23 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(
   }
 
   // RMSNorm over the row: var = mean(x^2) in fp32, x * rsqrt(var + eps) rounded to the
-  // dtype, times the weight (rounded).
-  const uint16_t* w = is_q ? qw : kw;
-  if (w != nullptr) {
+  // dtype, times the weight (rounded).  Computed whatever w is and selected after, so that
+  // the weight load has a use outside any branch (the compiler sinks a load into the branch
+  // that uses it, behind the wait for x).
+  {
+    const bool norm = w != nullptr;
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
 #pragma unroll
     for (int m = 1; m < LPR; m <<= 1) ss += __int_as_float(static_cast<int>(shfl_xor_u32(__float_as_uint(ss), m)));
     const float inv = rsqrtf(ss / float(D) + eps);
-    const dsp_u32x4 wv = *reinterpret_cast<const dsp_u32x4*>(w + 8 * sub);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      f[2 * i] = r<Tag>(lo<Tag>(wv[i]) * r<Tag>(f[2 * i] * inv));
-      f[2 * i + 1] = r<Tag>(hi<Tag>(wv[i]) * r<Tag>(f[2 * i + 1] * inv));
+      const float a = r<Tag>(lo<Tag>(wv[i]) * r<Tag>(f[2 * i] * inv));
+      const float b = r<Tag>(hi<Tag>(wv[i]) * r<Tag>(f[2 * i + 1] * inv));
+      f[2 * i] = norm ? a : f[2 * i];
+      f[2 * i + 1] = norm ? b : f[2 * i + 1];
     }
   }
 
@@ -114,8 +134,6 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(
     pr[2 * i + 1] = hi<Tag>(o);
   }
   const bool first_half = sub < LPR / 2;
-  const dsp_u32x4 cv = *reinterpret_cast<const dsp_u32x4*>(cosp + t * rst + 8 * sub);
-  const dsp_u32x4 sv = *reinterpret_cast<const dsp_u32x4*>(sinp + t * rst + 8 * sub);
   dsp_u32x4 out;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -129,21 +147,21 @@ __global__ __launch_bounds__(256) void qk_prologue_kernel(
     }
     out[i] = uint32_t(rnd<Tag>(o2[0])) | (uint32_t(rnd<Tag>(o2[1])) << 16);
   }
-  if (!live) return;
 
-  if (is_q) {
-    *reinterpret_cast<dsp_u32x4*>(qo + t * qost + int64_t(j) * qosh + 8 * sub) = out;
-    return;
-  }
-  const int64_t slot = slots[t];
-  if (slot < 0 || slot >= num_slots) {
-    if (sub == 0 && err_count) atomicAdd(err_count, 1);
-    return;
-  }
-  const int64_t pe = slot * pss + int64_t(kh) * psh + 8 * sub;
-  *reinterpret_cast<dsp_u32x4*>(kpool + pe) = out;
-  *reinterpret_cast<dsp_u32x4*>(vpool + pe) =
-      *reinterpret_cast<const dsp_u32x4*>(v + t * vst + int64_t(kh) * vsh + 8 * sub);
+  // Two stores per lane, neither under a branch (else the compiler sinks the loads that only
+  // they use behind the waits of the steps above): a q row to q_out, a k row and its v row
+  // to the token's pool slot; a lane past the rows, a k row whose slot is out of range and
+  // a q lane's v store write into g_prologue_drop instead.  Bad slots are counted after.
+  const bool slot_ok = slot >= 0 && slot < num_slots;
+  uint16_t* const drop = g_prologue_drop + 8 * threadIdx.x;
+  const int64_t pe = (slot_ok ? slot : 0) * pss + int64_t(is_q ? 0 : kh) * psh + 8 * sub;
+  uint16_t* const o_dst = !live  ? drop
+                          : is_q ? qo + t * qost + int64_t(j) * qosh + 8 * sub
+                          : slot_ok ? kpool + pe
+                                    : drop;
+  *reinterpret_cast<dsp_u32x4*>(o_dst) = out;
+  *reinterpret_cast<dsp_u32x4*>(live && !is_q && slot_ok ? vpool + pe : drop) = vrow;
+  if (live && !is_q && !slot_ok && sub == 0 && err_count) atomicAdd(err_count, 1);
 }
 
 // fp32 models: the same prologue with 4 elements per 16-byte lane (D/4 lanes per row) and
