@@ -310,34 +310,40 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
 }
 
 // Merge the key partitions of one (tile, KV head, sequence).  Grid = (tiles * 16 / R, KVH,
-// B) with R = 256 / D rows per workgroup: one thread per (row, dim) output.  Every thread
-// folds its row's partitions itself, 16 at a time with a running maximum, so the merge
-// waits on one memory round trip: the first 16 partitions' (max, sum) pairs and its
-// accumulator elements are loaded together with the sequence's lengths, before it is
-// known how many of them the row has (all lie inside the workspace; those past the row's
-// count, possibly never written, are discarded by a select, not weighted).
+// B), R = mq_combine_rows(D) rows per workgroup: one thread per (row, 4 dims) output, its
+// accumulator elements one 16-byte load per partition.  Every thread folds its row's
+// partitions itself, 16 at a time with a running maximum, so the merge waits on one memory
+// round trip: the first 16 partitions' (max, sum) pairs and its accumulator elements are
+// loaded together with the sequence's lengths, before it is known how many of them the
+// row has (all lie inside the workspace; those past the row's count, possibly never
+// written, are discarded by a select, not weighted).
+constexpr int mq_combine_rows(int D) { return 1024 / D < 16 ? 1024 / D : 16; }
+
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void mq_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
     int32_t G, int32_t P, int32_t num_parts, int32_t tiles_max, int32_t prefix_tokens,
     uint16_t* __restrict__ out, int64_t ost, int64_t osh) {
-  constexpr int R = 256 / D;   // rows per workgroup
-  constexpr int kBatch = 16;   // partitions in flight per thread
+  constexpr int TPR = D / 4;                // threads per row
+  constexpr int R = mq_combine_rows(D);     // rows per workgroup
+  constexpr int kBatch = 16;                // partitions in flight per thread
+  if (threadIdx.x >= R * TPR) return;       // D 32: 128 of the 256 threads
   const int tile = blockIdx.x / (16 / R), rsub = blockIdx.x % (16 / R);
   const int kvh = blockIdx.y, b = blockIdx.z, KVH = gridDim.y;
-  const int rl = threadIdx.x / D, d = threadIdx.x % D;
+  const int rl = threadIdx.x / TPR, d = 4 * (threadIdx.x % TPR);
   const int rr = rsub * R + rl;
   const int64_t slot0 = ((int64_t(b) * KVH + kvh) * tiles_max + tile) * num_parts;
   const float* src = ws_acc + (slot0 * 16 + rr) * D + d;
   const float* mlp = ws_ml + 2 * (slot0 * 16 + rr);
   constexpr int64_t kAccStride = int64_t(16) * D, kMlStride = 32;  // floats per partition
-  float va[kBatch], vm[kBatch], vl[kBatch];
+  f32x4 va[kBatch];
+  float vm[kBatch], vl[kBatch];
   auto load = [&](int p0, int n) {
 #pragma unroll
     for (int u = 0; u < kBatch; ++u)
       if (u < n) {
-        va[u] = src[(p0 + u) * kAccStride];
+        va[u] = *reinterpret_cast<const f32x4*>(src + (p0 + u) * kAccStride);
         vm[u] = mlp[(p0 + u) * kMlStride];
         vl[u] = mlp[(p0 + u) * kMlStride + 1];
       }
@@ -357,7 +363,8 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
   const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
   const int row = r0 + rr;
   if (nparts <= 1 || row >= rows) return;  // nparts 1: written by the attention kernel
-  float M = -INFINITY, L = 0.f, A = 0.f;
+  float M = -INFINITY, L = 0.f;
+  f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int p0 = 0; p0 < nparts; p0 += kBatch) {
     const int n = min(nparts - p0, kBatch);
     if (p0 > 0) load(p0, n);
@@ -373,13 +380,16 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
     for (int u = 0; u < kBatch; ++u) {
       const float w = u < n ? dsp_exp2(vm[u] - Mu) : 0.f;
       L = fmaf(u < n ? vl[u] : 0.f, w, L);
-      A = fmaf(u < n ? va[u] : 0.f, w, A);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) A[e] = fmaf(u < n ? va[u][e] : 0.f, w, A[e]);
     }
     M = Mn;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   const int qrow = q0 + row / G, hh = kvh * G + row % G;
-  out[int64_t(qrow) * ost + int64_t(hh) * osh + d] = narrow<Tag>(A * inv);
+  uint16_t* o = out + int64_t(qrow) * ost + int64_t(hh) * osh + d;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = narrow<Tag>(A[e] * inv);
 }
 
 template <typename Tag, bool kDecode = false, typename... A>
@@ -636,7 +646,7 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                              oh, o_stride_t, o_stride_h, err_count);
   }
   if (st != DSP_OK || ws_parts <= 1) return st;
-  dim3 cgrid(static_cast<unsigned>(tiles * 16 / (256 / D)), static_cast<unsigned>(KVH),
+  dim3 cgrid(static_cast<unsigned>(tiles * 16 / mq_combine_rows(D)), static_cast<unsigned>(KVH),
              static_cast<unsigned>(B));
   if (!f16)
     return launch_mq_combine<Bf16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
