@@ -283,77 +283,86 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(
 }
 
 // Log-sum-exp merge of the partitions of each (sequence, query head).
-// One wave per (sequence, head), four heads per workgroup: grid = (ceil(Hq/4), B).
-// Lanes first run over partitions (max of m, partition weights 2^(m_p - M), and their
-// l-weighted sum), the weights go through the wave's LDS row, then lanes run over dims
-// and stream the partial accumulators, eight partitions' loads issued before their FMAs.
+// One wave per (sequence, head), four heads per workgroup: grid = (ceil(Hq/4), B).  A lane
+// holds 4 dims of the output row (D/4 lanes per row), so the wave's 64/(D/4) lane groups
+// take interleaved partitions; each lane loads the (max, sum) pairs and accumulator
+// elements of 16 partitions before folding them in with a running maximum -- the first 16
+// together with the sequence's length, before it is known how many partitions there are
+// (all lie inside the workspace; those past the count are discarded by a select) -- and
+// the lane groups' results are merged by shuffles at the end.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void decode_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ ctx_lens, int32_t max_ctx, int32_t P, int32_t num_parts,
     int32_t Hq, uint16_t* __restrict__ out, int64_t osb, int64_t osh) {
-  constexpr int NV = D > 64 ? 2 : 1;  // dims per lane: lane, lane + 64
-  __shared__ float s_w[4][64];
+  constexpr int TPR = D / 4;        // lanes per output row
+  constexpr int S = 64 / TPR;       // lane groups: partitions folded side by side
+  constexpr int kBatch = 16;        // partitions in flight per lane
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h = blockIdx.x * 4 + wave, b = blockIdx.y;
   if (h >= Hq) return;
+  const int grp = lane / TPR, d = 4 * (lane % TPR);
+  const int64_t row0 = (int64_t(b) * Hq + h) * num_parts;
+  const float* src = ws_acc + row0 * D + d;
+  const float* mlp = ws_ml + 2 * row0;
+  f32x4 va[kBatch];
+  float vm[kBatch], vl[kBatch];
+  auto load = [&](int p0, int n) {  // partitions p0 + grp + S*u, u < kBatch, below n
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int p = p0 + grp + S * u;
+      if (p < n) {
+        va[u] = *reinterpret_cast<const f32x4*>(src + int64_t(p) * D);
+        vm[u] = mlp[2 * p];
+        vl[u] = mlp[2 * p + 1];
+      }
+    }
+  };
+  load(0, min(num_parts, S * kBatch));
   int ctx = ctx_lens[b];
   ctx = ctx < 0 ? 0 : (ctx > max_ctx ? max_ctx : ctx);
   const int nparts = ctx > 0 ? (ctx + P - 1) / P : 1;
   if (nparts <= 1) return;  // written directly by the partition kernel
-  const int64_t row0 = (int64_t(b) * Hq + h) * num_parts;
-  float M = -INFINITY;
-  for (int p = lane; p < nparts; p += 64) M = fmaxf(M, ws_ml[2 * (row0 + p)]);
+  float M = -INFINITY, L = 0.f;
+  f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int p0 = 0; p0 < nparts; p0 += S * kBatch) {
+    if (p0 > 0) load(p0, nparts);
+    float bm = M;
 #pragma unroll
-  for (int mask = 1; mask < 64; mask <<= 1) M = fmaxf(M, dsp_shfl_xor(M, mask));
-  const float Mu = M == -INFINITY ? 0.f : M;
-  const bool act = lane < D;
-  float L = 0.f, A[NV];
+    for (int u = 0; u < kBatch; ++u) bm = p0 + grp + S * u < nparts ? fmaxf(bm, vm[u]) : bm;
+    const float Mu = bm == -INFINITY ? 0.f : bm;
+    const float keep = dsp_exp2(M - Mu);  // 0 while nothing has been folded (M = -inf)
+    L *= keep;
+    A *= keep;
 #pragma unroll
-  for (int j = 0; j < NV; ++j) A[j] = 0.f;
-  for (int p0 = 0; p0 < nparts; p0 += 64) {
-    const int p = p0 + lane;
-    float w = 0.f;
-    if (p < nparts) {
-      w = dsp_exp2(ws_ml[2 * (row0 + p)] - Mu);
-      L = fmaf(ws_ml[2 * (row0 + p) + 1], w, L);
+    for (int u = 0; u < kBatch; ++u) {
+      const bool in = p0 + grp + S * u < nparts;
+      const float w = in ? dsp_exp2(vm[u] - Mu) : 0.f;
+      L = fmaf(in ? vl[u] : 0.f, w, L);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) A[e] = fmaf(in ? va[u][e] : 0.f, w, A[e]);
     }
-    s_w[wave][lane] = w;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int np = min(64, nparts - p0);
-    const float* src = ws_acc + (row0 + p0) * D + (act ? lane : 0);
-    int k = 0;
-    for (; k + 8 <= np; k += 8) {
-      float v[8][NV];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int j = 0; j < NV; ++j) v[u][j] = src[int64_t(k + u) * D + 64 * j];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float wk = s_w[wave][k + u];
-#pragma unroll
-        for (int j = 0; j < NV; ++j) A[j] = fmaf(v[u][j], wk, A[j]);
-      }
-    }
-    for (; k < np; ++k) {
-      const float wk = s_w[wave][k];
-#pragma unroll
-      for (int j = 0; j < NV; ++j) A[j] = fmaf(src[int64_t(k) * D + 64 * j], wk, A[j]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    M = bm;
   }
+  // merge the lane groups: group g's lane i meets group g ^ m's lane i
 #pragma unroll
-  for (int mask = 1; mask < 64; mask <<= 1) L += dsp_shfl_xor(L, mask);
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  uint16_t* o = out + int64_t(b) * osb + int64_t(h) * osh;
-  if (act) {
+  for (int m = TPR; m < 64; m <<= 1) {
+    const float Mo = dsp_shfl_xor(M, m), Lo = dsp_shfl_xor(L, m);
+    const float Mn = fmaxf(M, Mo);
+    const float Mu = Mn == -INFINITY ? 0.f : Mn;
+    const float ws = dsp_exp2(M - Mu), wo = dsp_exp2(Mo - Mu);
+    L = fmaf(L, ws, Lo * wo);
 #pragma unroll
-    for (int j = 0; j < NV; ++j) o[lane + 64 * j] = narrow<Tag>(A[j] * inv);
+    for (int e = 0; e < 4; ++e) A[e] = fmaf(A[e], ws, dsp_shfl_xor(A[e], m) * wo);
+    M = Mn;
+  }
+  if (grp == 0) {
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    uint16_t* o = out + int64_t(b) * osb + int64_t(h) * osh + d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = narrow<Tag>(A[e] * inv);
   }
 }
 
