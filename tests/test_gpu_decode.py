@@ -162,6 +162,30 @@ def test_split_k_partitions_agree(hip, P):
     assert_attention_close(f64(out), ref, f"P={P}")
 
 
+@pytest.mark.parametrize("D,P,ctx", [(16, 128, 33000), (32, 64, 8300), (64, 64, 4200),
+                                     (128, 64, 2200)])
+def test_merge_of_more_partitions_than_one_round(hip, D, P, ctx):
+    """The fixed-partition merge folds 16 partitions per lane and 64 / (D/4) lane groups
+    side by side per round: these contexts need more than one round (259, 130, 66 and 35
+    partitions), beside a sequence that needs none."""
+    from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
+    Hq, KVH, bs = 4, 2, 16
+    lens = [ctx, 40]
+    NB = sum(-(-n // bs) for n in lens) + 2
+    tables = random_block_tables(NB, lens, bs, 300 + D)
+    kc, vc = randn((NB * bs, KVH, D), 301 + D), randn((NB * bs, KVH, D), 302 + D)
+    q = randn((2, Hq, D), 303 + D)
+    bt = torch.zeros((2, max(len(t) for t in tables)), dtype=torch.int32)
+    for i, t in enumerate(tables):
+        bt[i, :len(t)] = torch.tensor(t)
+    out = paged_decode_attention_blocks(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV),
+                                        torch.tensor(lens, dtype=torch.int32).to(DEV),
+                                        Hq // KVH, partition_tokens=P)
+    st = _slot_table(tables, lens, bs, max(lens))
+    ref = ref_cpu.decode_attention(f64(q), f64(kc), f64(vc), st.numpy(), lens, Hq // KVH)
+    assert_attention_close(f64(out), ref, f"D={D} P={P}")
+
+
 def test_context_zero_gives_zeros_and_bad_ctx_is_reported(hip):
     from dispec_amd import _lib
     from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
