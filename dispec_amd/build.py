@@ -65,9 +65,26 @@ def _link(objs: list[Path], lib: Path, verbose: bool) -> Path:
     return lib
 
 
+def _build_fastcall(verbose: bool) -> Path:
+    """csrc/fastcall.c -> the CPython module dispec_amd._fastcall (gcc; host code only)."""
+    import sysconfig
+    out = PKG / ("_fastcall" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = ["gcc", "-O2", "-shared", "-fPIC", "-Wall", "-I", sysconfig.get_paths()["include"],
+           str(CSRC / "fastcall.c"), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"gcc failed on fastcall.c:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
+    return out
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every csrc/*.hip into libdispec_hip.so (the product library) and every
-    probe/*.hip into libdispec_probe.so (bench-side).  Returns the product library path."""
+    """Compile every csrc/*.hip into libdispec_hip.so (the product library), every
+    probe/*.hip into libdispec_probe.so (bench-side) and csrc/fastcall.c into the
+    dispec_amd._fastcall module.  Returns the product library path."""
     sources = sorted(CSRC.glob("*.hip"))
     probes = sorted(PROBE_SRC.glob("*.hip"))
     if not sources:
@@ -78,6 +95,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
         objs = list(pool.map(lambda s: _compile(s, verbose), sources + probes))
     if probes:
         _link(objs[len(sources):], PROBE_LIB, verbose)
+    _build_fastcall(verbose)
     return _link(objs[:len(sources)], LIB, verbose)
 
 

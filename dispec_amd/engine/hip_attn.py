@@ -82,7 +82,7 @@ def _decode(q, k_cache, v_cache, ctx_lens, kv_groups, scale, *, slot_table=None,
     out = torch.empty_like(q) if out is None else out
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
         raise ValueError("out must have q's shape and dtype with head_dim contiguous")
-    L = _lib.lib()
+    L = _lib.calls()
     P = int(partition_tokens)  # 0: the library's automatic split
     stream = _lib.stream_of(q)
     need = _decode_ws_bytes(B, Hq, KVH, D, int(max_ctx), P)
@@ -148,7 +148,7 @@ def decode_workspace(batch, num_heads, num_kv_heads, head_dim, max_ctx, device):
     """A float32 split-K workspace big enough for every decode launch of this shape (the
     automatic split), or None when the launch needs none.  One buffer serves all layers of
     a forward: the launches run in stream order."""
-    L = _lib.lib()
+    L = _lib.calls()
     need = L.dsp_paged_decode_workspace_bytes(batch, num_heads, num_kv_heads, head_dim,
                                               max_ctx, 0)
     return torch.empty(need // 4 + 1, dtype=torch.float32, device=device) if need else None
@@ -159,7 +159,7 @@ def mq_workspace(batch, num_heads, num_kv_heads, head_dim, max_q_len, max_ctx, d
     """A float32 split-K workspace for every `paged_mq_attention` launch of this shape with
     the automatic partition (or the balanced split), or None when it needs none.  One
     buffer serves all layers of a forward: the launches run in stream order."""
-    L = _lib.lib()
+    L = _lib.calls()
     if shared_prefix_tokens:
         P = L.dsp_paged_mq_shared_prefix_partition_tokens(
             batch, num_heads, num_kv_heads, head_dim, max_q_len, max_ctx, shared_prefix_tokens)
@@ -226,7 +226,7 @@ def paged_mq_attention(q, k_cache, v_cache, block_table, cu_q, ctx_lens, kv_grou
     out = torch.empty_like(q) if out is None else out
     if out.shape != q.shape or out.dtype != q.dtype or out.stride(2) != 1:
         raise ValueError("out must have q's shape and dtype with head_dim contiguous")
-    L = _lib.lib()
+    L = _lib.calls()
     sp = int(shared_prefix_tokens)
     if balanced and (sp or partition_tokens):
         raise ValueError("balanced excludes shared_prefix_tokens and partition_tokens")

@@ -66,7 +66,7 @@ def qk_norm_rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: 
     if out is None:
         out = torch.empty((T, Hq, D), dtype=dt, device=q.device)
     kl, vl = cache.key[layer_idx], cache.value[layer_idx]
-    _lib.check(_lib.lib().dsp_qk_norm_rope_append(
+    _lib.check(_lib.calls().dsp_qk_norm_rope_append(
         q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
         v.data_ptr(), v.stride(0), v.stride(1), _lib.ptr(qw), _lib.ptr(kw), eps,
         cos.data_ptr(), sin.data_ptr(), cos.stride(0), slots.data_ptr(), T, Hq, KVH, D,

@@ -128,7 +128,7 @@ class PagedKVCache:
         if k.stride(0) != v.stride(0):
             k, v = k.contiguous(), v.contiguous()
         slots = self._as_slots(slots.reshape(-1), self.key.device)
-        _lib.check(_lib.lib().dsp_kv_append(
+        _lib.check(_lib.calls().dsp_kv_append(
             self.key[layer_idx].data_ptr(), self.value[layer_idx].data_ptr(), self.num_slots,
             self.row_bytes, k.data_ptr(), v.data_ptr(), k.stride(0) * k.element_size(),
             slots.data_ptr(), n, self.row_bytes, self._err.data_ptr(), self._stream()),
