@@ -82,6 +82,14 @@ class PagedKVCache:
     def _stream(self) -> int:
         return _lib.stream_of(self.key)
 
+    def _layer_ptrs(self, layer_idx: int) -> tuple[int, int]:
+        """Device addresses of layer `layer_idx` of the K and V pools: what
+        key[layer_idx].data_ptr() gives, without building the two views per call."""
+        if not -self.num_layers <= layer_idx < self.num_layers:
+            raise IndexError(f"layer {layer_idx} is out of range for {self.num_layers} layers")
+        off = (layer_idx % self.num_layers) * self.layer_bytes
+        return self.key.data_ptr() + off, self.value.data_ptr() + off
+
     # -- error reporting -----------------------------------------------------------
     def check_errors(self) -> None:
         """Raise IndexError if any kernel met an out-of-range slot or block id."""
@@ -128,11 +136,12 @@ class PagedKVCache:
         if k.stride(0) != v.stride(0):
             k, v = k.contiguous(), v.contiguous()
         slots = self._as_slots(slots.reshape(-1), self.key.device)
+        kp, vp = self._layer_ptrs(layer_idx)
+        rb = self.row_bytes
         _lib.check(_lib.calls().dsp_kv_append(
-            self.key[layer_idx].data_ptr(), self.value[layer_idx].data_ptr(), self.num_slots,
-            self.row_bytes, k.data_ptr(), v.data_ptr(), k.stride(0) * k.element_size(),
-            slots.data_ptr(), n, self.row_bytes, self._err.data_ptr(), self._stream()),
-            "dsp_kv_append")
+            kp, vp, self.num_slots, rb, k.data_ptr(), v.data_ptr(),
+            k.stride(0) * k.element_size(), slots.data_ptr(), n, rb, self._err.data_ptr(),
+            self._stream()), "dsp_kv_append")
         self._after()
 
     def gather(self, layer_idx: int, slots: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
