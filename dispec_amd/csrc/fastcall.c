@@ -6,7 +6,8 @@
  * dispec_amd._lib (device pointers and sizes as Python ints, None for a null pointer, the
  * scale as a float) and call the library's entry points through the addresses that
  * dispec_amd._lib hands to bind(), so both paths reach the same loaded libdispec_hip.so.
- * Each returns the entry point's int status.  Built with gcc (no device code).
+ * Each returns the entry point's int status and, like ctypes, releases the GIL for the
+ * duration of the call.  Built with gcc (no device code).
  */
 #define PY_SSIZE_T_CLEAN
 #include <Python.h>
@@ -94,11 +95,15 @@ static PyObject* w_decode(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   arg_t v[32];
   UNBOUND(p_decode, "dsp_paged_decode");
   if (!convert("dsp_paged_decode", kDecodeSig, a, n, v)) return NULL;
-  return PyLong_FromLong(p_decode(v[0].p, v[1].q, v[2].q, v[3].p, v[4].p, v[5].q, v[6].q,
-                                  v[7].q, v[8].p, v[9].q, v[10].i, v[11].p, v[12].q, v[13].p,
-                                  v[14].i, v[15].i, v[16].i, v[17].i, v[18].f, v[19].i, v[20].i,
-                                  v[21].p, v[22].z, v[23].p, v[24].q, v[25].q, v[26].i, v[27].p,
-                                  v[28].p));
+  int st;
+  Py_BEGIN_ALLOW_THREADS
+  st = p_decode(v[0].p, v[1].q, v[2].q, v[3].p, v[4].p, v[5].q, v[6].q,
+                v[7].q, v[8].p, v[9].q, v[10].i, v[11].p, v[12].q, v[13].p,
+                v[14].i, v[15].i, v[16].i, v[17].i, v[18].f, v[19].i, v[20].i,
+                v[21].p, v[22].z, v[23].p, v[24].q, v[25].q, v[26].i, v[27].p,
+                v[28].p);
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(st);
 }
 
 static const char kAppendSig[] = "PPqqPPqPqqPP";
@@ -106,8 +111,12 @@ static PyObject* w_append(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   arg_t v[16];
   UNBOUND(p_append, "dsp_kv_append");
   if (!convert("dsp_kv_append", kAppendSig, a, n, v)) return NULL;
-  return PyLong_FromLong(p_append(v[0].p, v[1].p, v[2].q, v[3].q, v[4].p, v[5].p, v[6].q,
-                                  v[7].p, v[8].q, v[9].q, v[10].p, v[11].p));
+  int st;
+  Py_BEGIN_ALLOW_THREADS
+  st = p_append(v[0].p, v[1].p, v[2].q, v[3].q, v[4].p, v[5].p, v[6].q,
+                v[7].p, v[8].q, v[9].q, v[10].p, v[11].p);
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(st);
 }
 
 static const char kMqSig[] = "PqqPPqqqPqiPPiiiifiiiPzPqqiPP";
@@ -115,10 +124,14 @@ static PyObject* w_mq(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   arg_t v[32];
   UNBOUND(p_mq, "dsp_paged_mq_attention");
   if (!convert("dsp_paged_mq_attention", kMqSig, a, n, v)) return NULL;
-  return PyLong_FromLong(p_mq(v[0].p, v[1].q, v[2].q, v[3].p, v[4].p, v[5].q, v[6].q, v[7].q,
-                              v[8].p, v[9].q, v[10].i, v[11].p, v[12].p, v[13].i, v[14].i,
-                              v[15].i, v[16].i, v[17].f, v[18].i, v[19].i, v[20].i, v[21].p,
-                              v[22].z, v[23].p, v[24].q, v[25].q, v[26].i, v[27].p, v[28].p));
+  int st;
+  Py_BEGIN_ALLOW_THREADS
+  st = p_mq(v[0].p, v[1].q, v[2].q, v[3].p, v[4].p, v[5].q, v[6].q, v[7].q,
+            v[8].p, v[9].q, v[10].i, v[11].p, v[12].p, v[13].i, v[14].i,
+            v[15].i, v[16].i, v[17].f, v[18].i, v[19].i, v[20].i, v[21].p,
+            v[22].z, v[23].p, v[24].q, v[25].q, v[26].i, v[27].p, v[28].p);
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(st);
 }
 
 static const char kMqSpSig[] = "PqqPPqqqPqiPPiiiifiiiiPzPqqiPP";
@@ -126,11 +139,15 @@ static PyObject* w_mq_sp(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   arg_t v[32];
   UNBOUND(p_mq_sp, "dsp_paged_mq_attention_shared_prefix");
   if (!convert("dsp_paged_mq_attention_shared_prefix", kMqSpSig, a, n, v)) return NULL;
-  return PyLong_FromLong(p_mq_sp(v[0].p, v[1].q, v[2].q, v[3].p, v[4].p, v[5].q, v[6].q,
-                                 v[7].q, v[8].p, v[9].q, v[10].i, v[11].p, v[12].p, v[13].i,
-                                 v[14].i, v[15].i, v[16].i, v[17].f, v[18].i, v[19].i, v[20].i,
-                                 v[21].i, v[22].p, v[23].z, v[24].p, v[25].q, v[26].q, v[27].i,
-                                 v[28].p, v[29].p));
+  int st;
+  Py_BEGIN_ALLOW_THREADS
+  st = p_mq_sp(v[0].p, v[1].q, v[2].q, v[3].p, v[4].p, v[5].q, v[6].q,
+               v[7].q, v[8].p, v[9].q, v[10].i, v[11].p, v[12].p, v[13].i,
+               v[14].i, v[15].i, v[16].i, v[17].f, v[18].i, v[19].i, v[20].i,
+               v[21].i, v[22].p, v[23].z, v[24].p, v[25].q, v[26].q, v[27].i,
+               v[28].p, v[29].p);
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(st);
 }
 
 static const char kPrologueSig[] = "PqqPqqPqqPPfPPqPqiiiPqqPPqqqiPP";
@@ -138,11 +155,15 @@ static PyObject* w_prologue(PyObject* self, PyObject* const* a, Py_ssize_t n) {
   arg_t v[32];
   UNBOUND(p_prologue, "dsp_qk_norm_rope_append");
   if (!convert("dsp_qk_norm_rope_append", kPrologueSig, a, n, v)) return NULL;
-  return PyLong_FromLong(p_prologue(v[0].p, v[1].q, v[2].q, v[3].p, v[4].q, v[5].q, v[6].p,
-                                    v[7].q, v[8].q, v[9].p, v[10].p, v[11].f, v[12].p, v[13].p,
-                                    v[14].q, v[15].p, v[16].q, v[17].i, v[18].i, v[19].i,
-                                    v[20].p, v[21].q, v[22].q, v[23].p, v[24].p, v[25].q, v[26].q,
-                                    v[27].q, v[28].i, v[29].p, v[30].p));
+  int st;
+  Py_BEGIN_ALLOW_THREADS
+  st = p_prologue(v[0].p, v[1].q, v[2].q, v[3].p, v[4].q, v[5].q, v[6].p,
+                  v[7].q, v[8].q, v[9].p, v[10].p, v[11].f, v[12].p, v[13].p,
+                  v[14].q, v[15].p, v[16].q, v[17].i, v[18].i, v[19].i,
+                  v[20].p, v[21].q, v[22].q, v[23].p, v[24].p, v[25].q, v[26].q,
+                  v[27].q, v[28].i, v[29].p, v[30].p);
+  Py_END_ALLOW_THREADS
+  return PyLong_FromLong(st);
 }
 
 /* bind(name, address): the entry point `name` of the loaded library is at `address`. */
