@@ -32,6 +32,33 @@ from dispec_amd.kv.block_manager import BlockManager
 _CHECK_EVERY_CALL = os.environ.get("DISPEC_HIP_CHECK", "0") not in ("", "0")
 
 
+def check_prefix_kv(cache, prefix_kv, prompt_len: int) -> None:
+    """Validate transferred KV before a request is admitted with it.
+
+    The admission check of the reference scheduler (dispec/sched/scheduler.py:103-112):
+    `prefix_kv` = (k, v), each (num_layers, T, num_kv_heads, head_dim) of `cache`'s
+    layout, must cover at least one and fewer than all of the prompt's tokens -- the
+    last prompt token is forwarded by the target itself to produce the first output
+    token's logits.  Only the geometry attributes of `cache` are read, so the check runs
+    on the host before anything reaches the GPU.  The messages are the reference's:
+    callers and tests match on them.
+    """
+    k, v = prefix_kv
+    covered = k.shape[1] if k.dim() > 1 else -1
+    layout = (cache.num_layers, covered, cache.num_kv_heads, cache.head_dim)
+    if tuple(k.shape) != layout or tuple(v.shape) != layout:
+        raise ValueError(f"prefix_kv shapes {tuple(k.shape)}/{tuple(v.shape)} do not "
+                         f"match this model's cache layout {layout}")
+    check_prefix_coverage(covered, prompt_len)
+
+
+def check_prefix_coverage(covered: int, prompt_len: int) -> None:
+    """The coverage half of `check_prefix_kv`: 0 < covered < prompt_len."""
+    if not 0 < covered < prompt_len:
+        raise ValueError(f"prefix_kv covers {covered} tokens of a {prompt_len}-token "
+                         "prompt; it must cover at least one and fewer than all of them")
+
+
 class PagedKVCache:
     def __init__(self, num_layers: int, num_blocks: int, block_size: int, num_kv_heads: int,
                  head_dim: int, dtype: torch.dtype = torch.bfloat16, device: str = "cuda"):
@@ -246,6 +273,20 @@ class PagedKVCache:
         k = k.to(device=self.key.device, dtype=self.dtype)
         v = v.to(device=self.key.device, dtype=self.dtype)
         self.import_batch([block_ids], k, v, [0, k.shape[1]])
+
+    def check_prefix_kv(self, prefix_kv, prompt_len: int) -> None:
+        """Raise ValueError unless prefix_kv fits this cache and covers 0 < T < prompt_len
+        of the prompt (dispec/sched/scheduler.py:103-112)."""
+        check_prefix_kv(self, prefix_kv, prompt_len)
+
+    def admit_prefix(self, block_ids: list[int], prefix_kv, prompt_len: int) -> int:
+        """Admit a request with transferred KV: check it, scatter it into the request's
+        blocks and return the number of prompt tokens it covers -- the tokens the block
+        table now holds and the position prefill resumes from (scheduler.py:96-97,
+        :165-170)."""
+        self.check_prefix_kv(prefix_kv, prompt_len)
+        self.import_contiguous(block_ids, *prefix_kv)
+        return prefix_kv[0].shape[1]
 
     # -- device-table forms (no host round trip; what graph-captured callers use) ---------
     def gather_into(self, block_table: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,

@@ -29,6 +29,7 @@ from pathlib import Path
 import torch
 
 from dispec_amd import _lib
+from dispec_amd.kv.paged_cache import check_prefix_coverage
 
 KINDS = ("keys", "values")
 
@@ -187,7 +188,9 @@ class LayerMap:
         problem's rows into its blocks of one pool layer -- one GEMM launch writing straight
         into the pool (dsp_kv_map_gemm_to_pool).  Returns False, having done nothing, when
         this map or shape has no fused form (residual maps; shapes the large-tile GEMM does
-        not take): the caller then runs apply_into + RoPE + scatter."""
+        not take): the caller then runs apply_into + RoPE + scatter.  A row whose block id
+        lies outside the pool is skipped and counted in `err` (at least once per row: once
+        per 128-column tile of the row)."""
         self._prepare()
         if self.residual is not None:
             return False
@@ -197,6 +200,10 @@ class LayerMap:
             return False
         if self.factors is not None:
             r = self._lt.shape[0]
+            if r % 64:
+                # the fused launch steps K (= the rank here) 64 at a time: decide before the
+                # first GEMM runs, or the caller's fallback would run it a second time
+                return False
             tmp = torch.empty((batch, rows, r), dtype=torch.bfloat16, device=a.device)
             _gemm(a, seg_offsets, seg_len, lda, rows, self._lt, tmp, batch=batch,
                   a_batch_stride=a_batch_stride, c_batch_stride=rows * r)
