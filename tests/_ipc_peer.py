@@ -6,16 +6,20 @@ interpreter, never a fork or an exec of a process that has a GPU context.  For e
 it builds its own paged cache, receives one payload through HipIpcTransport, scatters it
 into randomly placed blocks of its cache with the import kernel, re-exports those blocks
 with the gather kernel and reports what it read back (bytes for small payloads, per-layer
-checksums for large ones).
+position-weighted checksums of every row for large ones).
 """
 
 from __future__ import annotations
 
 
-def _checksums(t):
+def _row_checksums(t):
+    """One int64 per (layer, token) row: sum over the row's int32 words of word * (i + 1).
+    Compared position by position, a moved, swapped or reordered row or word shows."""
     import torch
-    flat = t.reshape(t.shape[0], -1).contiguous().view(torch.int32).to(torch.int64)
-    return flat.sum(dim=1).tolist()
+    L, T = t.shape[0], t.shape[1]
+    words = t.contiguous().view(torch.int32).reshape(L, T, -1).to(torch.int64)
+    weight = torch.arange(1, words.shape[-1] + 1, dtype=torch.int64, device=t.device)
+    return (words * weight).sum(dim=-1).cpu().numpy()
 
 
 def serve(cmd_q, res_q, msg_q, ack_q) -> None:
@@ -44,7 +48,7 @@ def serve(cmd_q, res_q, msg_q, ack_q) -> None:
             if cmd["report"] == "bytes":
                 out = (k.view(torch.int16).cpu().numpy(), v.view(torch.int16).cpu().numpy())
             else:
-                out = (_checksums(k), _checksums(v))
+                out = (_row_checksums(k), _row_checksums(v))
             res_q.put({"ok": True, "shape": shape, "tokens": len(payload.tokens),
                        "meta": payload.meta, "result": out})
             del cache, k, v

@@ -69,7 +69,7 @@ def bf16_spacing(x) -> np.ndarray:
     return np.where(m > 0, np.exp2(e - 7), 0.0)
 
 
-def bf16_chain_bound(*stages, lipschitz: float = 1.0) -> np.ndarray:
+def bf16_chain_bound(*stages, lipschitz: float = 1.0, carry=0.0) -> np.ndarray:
     """Per-element bound on |got - ref| for two evaluations of one chain of bf16 roundings
     whose exact inputs agree up to fp32 accumulation order.
 
@@ -77,12 +77,21 @@ def bf16_chain_bound(*stages, lipschitz: float = 1.0) -> np.ndarray:
     order.  Two roundings of values that differ by e land at most e + one gap apart, and
     the gap at the next binade up is twice the gap at |x|, so each step adds 2 gaps at its
     magnitude; `lipschitz` bounds how much a step between roundings (e.g. gelu, |f'| <
-    1.13) can amplify the error carried into it.
+    1.13) can amplify the error carried into it.  `carry` is an error already present
+    before the first rounding (fp32 accumulation order, or an earlier chain's bound
+    pushed through a matrix product).
     """
-    bound = 0.0
+    bound = np.asarray(carry, np.float64)
     for m in stages:
         bound = lipschitz * bound + 2.0 * bf16_spacing(np.asarray(m, np.float64) * (1 + 2 ** -7))
     return bound
+
+
+def fp32_dot_slack(abs_a, abs_b) -> np.ndarray:
+    """Bound on how far two fp32 evaluations of a @ b (any summation order) can differ:
+    2 * K * 2^-24 * (|a| @ |b|) for an inner dimension K (Higham's gamma_K, twice)."""
+    abs_a, abs_b = np.asarray(abs_a, np.float64), np.asarray(abs_b, np.float64)
+    return 2.0 * abs_a.shape[-1] * 2.0 ** -24 * (abs_a @ abs_b)
 
 
 def assert_bf16_within(got_bits, ref_bits, bound, what, min_exact: float = 0.99) -> None:

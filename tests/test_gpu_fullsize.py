@@ -83,13 +83,13 @@ def test_config3_headline_batch_full_size(config3):
     for name, P in (("balanced", 0), ("fixed-512", 512)):
         outs[name] = paged_decode_attention_blocks(
             c["q"], c["kc"], c["vc"], c["bt"], ctx_lens, G, block_size=c["bs"],
-            max_ctx=c["ctx"], partition_tokens=P)
+            max_ctx=c["ctx"], partition_tokens=P, err=err)
     torch.cuda.synchronize()
     # the automatic split at this shape is the balanced kernel (the benchmark's route)
     L = _lib.lib()
     assert L.dsp_paged_decode_workspace_bytes(16, 32, 8, 128, 32768, 0) != \
         L.dsp_paged_decode_workspace_bytes(16, 32, 8, 128, 32768, 512)
-    assert int(err.item()) == 0
+    assert int(err.item()) == 0, "a launch met a bad block id or a clamped length"
     _check_decode_per_sequence(outs, c["q"], c["kc"], c["vc"], c["tables"], lens, G,
                                c["bs"], "config 3")
 
@@ -116,10 +116,12 @@ def test_config2_batch_full_size():
         bt[i, :len(t)] = torch.tensor(t, dtype=torch.int32)
     q = torch.randn((B, Hq, D), generator=torch.Generator().manual_seed(2004)).to(torch.bfloat16)
     lens = ctx.tolist()
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
     out = paged_decode_attention_blocks(q.to(DEV), kc, vc, bt.to(DEV),
                                         ctx.to(torch.int32).to(DEV), Hq // KVH, block_size=bs,
-                                        max_ctx=int(ctx.max()))
+                                        max_ctx=int(ctx.max()), err=err)
     torch.cuda.synchronize()
+    assert int(err.item()) == 0, "the launch met a bad block id or a clamped length"
     _check_decode_per_sequence({"automatic": out}, q, kc, vc, tables, lens, Hq // KVH, bs,
                                "config 2")
 

@@ -64,18 +64,24 @@ def test_small_ragged_payload_bit_exact(ipc_peer, copy_path):
         assert np.array_equal(got.view(np.uint16), ref)
 
 
-def _layer_checksums(a: np.ndarray) -> list[int]:
-    flat = np.ascontiguousarray(a).reshape(a.shape[0], -1).view(np.int32).astype(np.int64)
-    return flat.sum(axis=1).tolist()
+def _row_checksums(a: np.ndarray) -> np.ndarray:
+    """The peer's per-(layer, token) checksum: sum of int32 word * (index + 1) in int64."""
+    L, T = a.shape[0], a.shape[1]
+    words = np.ascontiguousarray(a).view(np.int32).reshape(L, T, -1).astype(np.int64)
+    return (words * np.arange(1, words.shape[-1] + 1, dtype=np.int64)).sum(axis=-1)
 
 
 def test_config5_request_payload(ipc_peer):
     """One config-5 request: Qwen3-1.7B geometry (28 layers, 8 KV heads of 128), 4096
     tokens -- 235 MB each of K and V in one region apiece -- checked per layer against
-    the oracle's export of the sender's pool (a checksum of each layer's bytes)."""
+    the oracle's export of the sender's pool, row by row: a position-weighted checksum of
+    each (layer, token) row's words, so a row landing in another row's place (the error a
+    scatter through the wrong block makes) fails at that row."""
     cache, ids = _source(28, 300, 16, 8, 128, 4096, 8300)
     k_sums, v_sums = _hand_off(ipc_peer, cache, ids, 4096, "checksum", 8400, request_id=1,
                                first_token=42)
     for got, pool in ((k_sums, cache.key), (v_sums, cache.value)):
-        ref = ref_cpu.export_contiguous(bits(pool), ids, 4096, 16)
-        assert got == _layer_checksums(ref)
+        ref = _row_checksums(ref_cpu.export_contiguous(bits(pool), ids, 4096, 16))
+        assert got.shape == (28, 4096)
+        bad = np.argwhere(got != ref)
+        assert bad.size == 0, f"{len(bad)} rows differ, first (layer, token) {bad[0].tolist()}"

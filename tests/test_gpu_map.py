@@ -17,7 +17,8 @@ import pytest
 import torch
 
 from oracle import ref_cpu
-from tests._util import assert_bf16_within, bf16_chain_bound, bits, gen, randn
+from tests._util import (assert_bf16_within, bf16_chain_bound, bits, fp32_dot_slack, gen,
+                         randn)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -168,36 +169,71 @@ def test_identity_map_reproduces_raw_kv():
     assert torch.equal(gk, kk) and torch.equal(gv, vv)
 
 
+def _stage(got, expect, *stages, carry=0.0, what=""):
+    """One rounding stage: the kernel's output against the oracle applied to the kernel's
+    own input, per element within its chain bound."""
+    assert_bf16_within(bits(got), ref_cpu.f32_to_bf16(np.asarray(expect, np.float32)),
+                       bf16_chain_bound(*stages, carry=carry), what)
+
+
 def test_factored_and_residual_forms():
-    from dispec_amd.kv.transfer import LayerMap
+    """The low-rank form bf16(bf16(bf16(x @ L) @ R) + b) and the residual form
+    bf16(y + bf16(bf16(gelu(bf16(x @ dw^T + db))) @ up^T)), checked stage by stage: each
+    GEMM launch against the oracle's rounding of the same stage applied to the kernel's own
+    input, every element within the bound of that stage's roundings (two bf16 gaps at each
+    value rounded, plus fp32 summation-order slack), so a near-zero output is held to its
+    own intermediates' magnitudes; and the whole map (LayerMap.apply) bit-identical to the
+    stages run one after the other."""
+    from dispec_amd.kv.transfer import LayerMap, _gemm
     g = gen(4)
     K, N, r, hidden, T = 128, 64, 16, 24, 77
     left, right = torch.randn(K, r, generator=g) / 8, torch.randn(r, N, generator=g) / 4
     bias = torch.randn(N, generator=g)
     x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    xg = x.to(DEV)
+    xd = x.double().numpy()
+    rnd = ref_cpu.round_bf16
+    f64 = lambda t: t.double().cpu().numpy()  # noqa: E731
+
     fac = LayerMap((0,), bias, factors=(left, right)).to(DEV, torch.bfloat16)
-    got = fac.apply(x.to(DEV)).float().cpu().numpy()
-    lb, rb, bb = (t.to(torch.bfloat16).double().numpy() for t in (left, right, bias))
-    mid = ref_cpu.round_bf16(x.double().numpy() @ lb)
-    expect = ref_cpu.round_bf16(ref_cpu.round_bf16(mid @ rb) + bb)
-    assert np.abs(got - expect).max() <= 2 * np.abs(expect).max() * 2 ** -8
+    got = fac.apply(xg)
+    lb, rb, bb = f64(fac.factors[0]), f64(fac.factors[1]), f64(fac.bias)
+    mid = _gemm(xg, [0], K, K, T, fac._lt, torch.empty((T, r), dtype=torch.bfloat16, device=DEV))
+    sl = fp32_dot_slack(np.abs(xd), np.abs(lb))
+    _stage(mid, rnd(xd @ lb), np.abs(xd @ lb) + sl, carry=sl, what="x @ L")
+    md = f64(mid)
+    sl = fp32_dot_slack(np.abs(md), np.abs(rb))
+    a = np.abs(md @ rb) + sl
+    _stage(got, rnd(rnd(md @ rb) + bb), a, a + np.abs(bb), carry=sl, what="(x @ L) @ R + b")
+    two = _gemm(mid, [0], r, r, T, fac._rt, torch.empty((T, N), dtype=torch.bfloat16, device=DEV),
+                fac._b, bias_mode=1)
+    assert torch.equal(got, two), "factored apply differs from its two GEMMs"
+
     dw, db, uw = torch.randn(hidden, K, generator=g) / 8, torch.randn(hidden, generator=g), \
         torch.randn(N, hidden, generator=g) / 4
     W = torch.randn(K, N, generator=g) / 8
     res = LayerMap((0,), bias, weight=W, residual=(dw, db, uw)).to(DEV, torch.bfloat16)
-    got = res.apply(x.to(DEV)).float().cpu().numpy()
-    xd = x.double().numpy()
-    Wb, dwb, dbb, uwb = (t.to(torch.bfloat16).double().numpy() for t in (W, dw, db, uw))
-    y = ref_cpu.round_bf16(ref_cpu.round_bf16(xd @ Wb) + bb)
-    h = ref_cpu.round_bf16(xd @ dwb.T + dbb)
-    h = ref_cpu.round_bf16(ref_cpu._gelu(h))
-    expect = ref_cpu.round_bf16(y + ref_cpu.round_bf16(h @ uwb.T))
-    assert np.abs(got - expect).max() <= 2 * np.abs(expect).max() * 2 ** -8
-    # use_residual=False is the plain affine map
-    plain = res.apply(x.to(DEV), use_residual=False)
-    a = np.abs(xd @ Wb)
-    assert_bf16_within(bits(plain), ref_cpu.f32_to_bf16(y.astype(np.float32)),
-                       bf16_chain_bound(a, a + np.abs(bb)), "plain affine")
+    got = res.apply(xg)
+    plain = res.apply(xg, use_residual=False)     # use_residual=False: the plain affine map
+    Wb, dwb, dbb, uwb = (f64(t) for t in (res.weight, *res.residual))
+    a = np.abs(xd @ Wb) + fp32_dot_slack(np.abs(xd), np.abs(Wb))
+    _stage(plain, rnd(rnd(xd @ Wb) + bb), a, a + np.abs(bb),
+           carry=fp32_dot_slack(np.abs(xd), np.abs(Wb)), what="x @ W + b")
+    h = _gemm(xg, [0], K, K, T, res._down[0], torch.empty((T, hidden), dtype=torch.bfloat16,
+                                                           device=DEV),
+              res._down[1], bias_mode=2, act=1)
+    pre = xd @ dwb.T + dbb
+    sl = fp32_dot_slack(np.abs(xd), np.abs(dwb.T))
+    e_pre = bf16_chain_bound(np.abs(pre) + sl, carry=sl)
+    act = ref_cpu._gelu(rnd(pre))
+    _stage(h, rnd(act), np.abs(act) + 1.13 * e_pre, carry=1.13 * e_pre, what="gelu(x @ dw^T + db)")
+    hd, yd = f64(h), f64(plain)
+    s_r = hd @ uwb.T
+    sl = fp32_dot_slack(np.abs(hd), np.abs(uwb.T))
+    a = np.abs(s_r) + sl
+    _stage(got, rnd(yd + rnd(s_r)), a, np.abs(yd) + a, carry=sl, what="y + up(h)")
+    both = _gemm(h, [0], hidden, hidden, T, res._up, plain.clone(), accumulate=True)
+    assert torch.equal(got, both), "residual apply differs from its GEMMs"
 
 
 @pytest.mark.parametrize("in_dtype", [torch.float32, torch.bfloat16])
@@ -247,6 +283,56 @@ def test_escalation_export_map_import_round_trip():
     other.import_contiguous(t2.block_ids, mk, mv)
     back = other.export_contiguous(t2.block_ids, 36)
     assert torch.equal(back[0], mk) and torch.equal(back[1], mv)
+
+
+def test_admitted_prefix_reproduces_the_prefill():
+    """A model's own KV for n-1 prompt tokens, raw and through an identity map, admitted
+    with admit_prefix (the check and import of the reference scheduler's admission), then
+    the last prompt token forwarded alone: its logits equal a plain prefill's
+    (tests/test_kv_transfer.py:234-252, the identity-injection gate).  In bf16 the one-row
+    and 37-row projections round differently, so the bar is cosine, not 1e-4."""
+    from dispec_amd.engine.model_runner import ModelRunner, SeqMeta
+    from dispec_amd.kv.paged_cache import PagedKVCache
+    from dispec_amd.kv.transfer import CrossModelKVMap, LayerMap
+    from dispec_amd.workers.escalation import admit_prefix, map_prefix
+    from tests.toy_lm import toy_lm
+    model = toy_lm("qwen3").to(torch.bfloat16).to(DEV)
+    cfg = model.config
+    runner = ModelRunner(model)
+    cache = PagedKVCache.for_model(cfg, 32, 16, torch.bfloat16, DEV)
+    n = 37
+    ids = torch.randint(0, 128, (n,), generator=gen(16)).tolist()
+
+    def prefill(sid):
+        table = cache.manager.allocate(sid, n)
+        h = runner.forward(torch.tensor(ids, device=DEV), torch.arange(n, device=DEV),
+                           cache.context_slots(table.block_ids, n),
+                           [SeqMeta(table.block_ids, n, n)], cache)
+        return table, runner.logits(h[-1:]).float()[0]
+
+    src, plain = prefill(1)
+    kvd = cfg.num_key_value_heads * cfg.head_dim
+    eye = lambda i: LayerMap((i,), torch.zeros(kvd), weight=torch.eye(kvd))  # noqa: E731
+    kmap = CrossModelKVMap([eye(i) for i in range(cfg.num_hidden_layers)],
+                           [eye(i) for i in range(cfg.num_hidden_layers)], cfg, cfg
+                           ).to(DEV, torch.bfloat16)
+    raw = cache.export_contiguous(src.block_ids, n - 1)
+    mapped = map_prefix(runner, cache, src.block_ids, n, kmap, runner)
+    for sid, prefix in ((2, raw), (3, mapped)):
+        table = admit_prefix(cache, sid, ids, prefix)
+        assert table.num_tokens == n - 1
+        assert torch.equal(cache.export_contiguous(table.block_ids, n - 1)[1], prefix[1])
+        slot = cache.context_slots(table.block_ids, n)[-1:]
+        table.num_tokens = n
+        h = runner.forward(torch.tensor(ids[-1:], device=DEV), torch.tensor([n - 1], device=DEV),
+                           slot, [SeqMeta(table.block_ids, 1, n)], cache)
+        got = runner.logits(h[-1:]).float()[0]
+        cosine = torch.nn.functional.cosine_similarity(got, plain, dim=0).item()
+        assert cosine >= 0.999, (sid, cosine)
+        assert int(got.argmax()) == int(plain.argmax())
+        cache.manager.free(sid)
+    with pytest.raises(ValueError, match="fewer than all"):
+        admit_prefix(cache, 4, ids[:-1], raw)
 
 
 @pytest.mark.parametrize("B,M,N,bias_mode,act,accum", [
@@ -361,22 +447,33 @@ def test_gemm_to_pool_equals_gemm_rope_scatter(D, rope, bad_block):
     assert (int(err.item()) > 0) == bad_block and (int(err_ref.item()) > 0) == bad_block
 
 
-@pytest.mark.parametrize("residual", [False, True])
-def test_map_into_equals_map_then_import(residual):
+@pytest.mark.parametrize("form", ["dense", "residual", "factored-128", "factored-96"])
+def test_map_into_equals_map_then_import(form, monkeypatch):
     """CrossModelKVMap.map_into (fused GEMM -> pool per target layer) leaves the target cache
     bit-identical to map() followed by import_contiguous (config-5 layer selection at a
-    small size); a map with a trained residual takes the unfused path per layer."""
+    small size).  A map with a trained residual takes the unfused path per layer; low-rank
+    maps take the fused launch for their second factor when the rank is a multiple of 64
+    (128) and the unfused path otherwise (96) -- deciding before the first factor's GEMM,
+    so no GEMM runs twice (counted)."""
+    from dispec_amd.kv import transfer
     from dispec_amd.kv.transfer import CrossModelKVMap, LayerMap
     L_src, L_tgt, H, D, T = 6, 8, 8, 128, 300
     kv = H * D
     pick = lambda i: [int(round(i * (L_src - 1) / (L_tgt - 1)))]  # noqa: E731
     maps = _maps(L_src, L_tgt, kv, 1, 31, scale=1 / 32, layer_fn=pick)
+    rank = int(form.split("-")[1]) if form.startswith("factored") else 0
 
     def layer_maps():
         out = []
-        for mm in maps:
-            lm = LayerMap(mm["source_layers"], mm["bias"], weight=mm["weight"])
-            if residual:
+        for i, mm in enumerate(maps):
+            if rank:
+                g = gen(40 + i)
+                lm = LayerMap(mm["source_layers"], mm["bias"],
+                              factors=(torch.randn(kv, rank, generator=g) / 32,
+                                       torch.randn(rank, kv, generator=g) / rank ** 0.5))
+            else:
+                lm = LayerMap(mm["source_layers"], mm["bias"], weight=mm["weight"])
+            if form == "residual":
                 g = gen(32)
                 lm.residual = (torch.randn(64, kv, generator=g) / 32, torch.randn(64, generator=g),
                                torch.randn(kv, 64, generator=g) / 8)
@@ -392,8 +489,13 @@ def test_map_into_equals_map_then_import(residual):
     ids = torch.randperm(64, generator=gen(36))[:-(-T // 16)].tolist()
     mk, mv = kmap.map(kk, vv, src_rope, tgt_rope)
     ref_c.import_contiguous(ids, mk, mv)
+    gemms = []
+    real_gemm = transfer._gemm
+    monkeypatch.setattr(transfer, "_gemm", lambda *a, **k: gemms.append(1) or real_gemm(*a, **k))
     kmap.map_into(kk, vv, src_rope, tgt_rope, got_c, ids)
     torch.cuda.synchronize()
     got_c.check_errors()
     assert torch.equal(got_c.key.view(torch.int16), ref_c.key.view(torch.int16))
     assert torch.equal(got_c.value.view(torch.int16), ref_c.value.view(torch.int16))
+    per_map = {"dense": 0, "residual": 3, "factored-128": 1, "factored-96": 2}[form]
+    assert len(gemms) == 2 * L_tgt * per_map, (form, len(gemms))
