@@ -117,9 +117,20 @@ def lib() -> ctypes.CDLL:
     return handle
 
 
+# ctypes argument type -> the type letter dispec_amd._fastcall converts it with
+_TYPE_LETTERS = {c_void_p: "P", c_int64: "q", c_int32: "i", c_size_t: "z", c_float: "f"}
+
+
+def type_letters(argtypes) -> str:
+    """The fast binding's signature string for a list of ctypes argtypes ('?' for a type
+    the fast binding does not convert)."""
+    return "".join(_TYPE_LETTERS.get(t, "?") for t in argtypes)
+
+
 class _Calls:
-    """Attribute access to the library's entry points: the fast binding where there is one,
-    the ctypes function otherwise (same arguments, same int status)."""
+    """Attribute access to the library's entry points: the fast binding where there is one
+    and its argument types equal the ctypes argtypes, the ctypes function otherwise (same
+    arguments, same int status)."""
 
     def __init__(self, handle: ctypes.CDLL):
         fast = None
@@ -127,11 +138,14 @@ class _Calls:
             from dispec_amd import _fastcall as fast
         except ImportError:
             fast = None
-        for name in SIGNATURES:
+        fast_sigs = getattr(fast, "SIGNATURES", {}) if fast is not None else {}
+        self.fast_bound: list[str] = []
+        for name, (_, argtypes) in SIGNATURES.items():
             fn = getattr(handle, name)
-            if fast is not None and name in FAST_CALLS:
+            if name in FAST_CALLS and fast_sigs.get(name) == type_letters(argtypes):
                 fast.bind(name, ctypes.cast(fn, c_void_p).value)
                 fn = getattr(fast, name)
+                self.fast_bound.append(name)
             setattr(self, name, fn)
 
 

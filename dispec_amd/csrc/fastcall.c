@@ -196,4 +196,37 @@ static PyMethodDef kMethods[] = {
 
 static struct PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_fastcall", NULL, -1, kMethods};
 
-PyMODINIT_FUNC PyInit__fastcall(void) { return PyModule_Create(&kModule); }
+/* The module exports SIGNATURES = {name: type letters}, the argument types each function
+ * converts, so the loader can compare them with its ctypes argtypes and refuse to bind a
+ * function whose prototype here has fallen out of step with the header. */
+PyMODINIT_FUNC PyInit__fastcall(void) {
+  static const struct {
+    const char* name;
+    const char* sig;
+  } kSigs[] = {{"dsp_paged_decode", kDecodeSig},
+               {"dsp_kv_append", kAppendSig},
+               {"dsp_paged_mq_attention", kMqSig},
+               {"dsp_paged_mq_attention_shared_prefix", kMqSpSig},
+               {"dsp_qk_norm_rope_append", kPrologueSig}};
+  PyObject* m = PyModule_Create(&kModule);
+  if (!m) return NULL;
+  PyObject* sigs = PyDict_New();
+  if (!sigs) goto fail;
+  for (size_t k = 0; k < sizeof(kSigs) / sizeof(kSigs[0]); ++k) {
+    PyObject* v = PyUnicode_FromString(kSigs[k].sig);
+    if (!v || PyDict_SetItemString(sigs, kSigs[k].name, v) < 0) {
+      Py_XDECREF(v);
+      Py_DECREF(sigs);
+      goto fail;
+    }
+    Py_DECREF(v);
+  }
+  if (PyModule_AddObject(m, "SIGNATURES", sigs) < 0) {
+    Py_DECREF(sigs);
+    goto fail;
+  }
+  return m;
+fail:
+  Py_DECREF(m);
+  return NULL;
+}

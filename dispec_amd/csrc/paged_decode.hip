@@ -26,6 +26,7 @@
 // for GQA groups of 6+); this VALU kernel serves per-token slot tables and head_dim 16.
 #include <float.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "dsp_common.h"
@@ -649,24 +650,31 @@ namespace {
 __device__ __align__(256) unsigned char scratch[DSP_NOALLOC_SCRATCH_BYTES];
 
 constexpr int kMaxScratchDevices = 64;
-std::once_flag g_scratch_once[kMaxScratchDevices];
-void* g_scratch_ptr[kMaxScratchDevices];
-int g_scratch_status[kMaxScratchDevices];
+std::mutex g_scratch_mu;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];
 
-// The current device's copy of `scratch` (status 0), set up on the first call per device.
+// The current device's copy of `scratch` (status 0).  The address is looked up on the
+// first call per device and kept only once the lookup succeeds, so a failed lookup (a
+// transient runtime error) is tried again on the next call instead of being returned for
+// the life of the process.
 int scratch_for_current_device(void** ptr) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return static_cast<int>(e);
   if (dev < 0 || dev >= kMaxScratchDevices) return DSP_EUNSUPPORTED;
-  std::call_once(g_scratch_once[dev], [dev] {
-    void* p = nullptr;
-    const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    g_scratch_status[dev] = r == hipSuccess ? (p ? DSP_OK : DSP_EINVAL) : static_cast<int>(r);
-    g_scratch_ptr[dev] = p;
-  });
-  *ptr = g_scratch_ptr[dev];
-  return g_scratch_status[dev];
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (r != hipSuccess) return static_cast<int>(r);
+      if (p == nullptr) return DSP_EINVAL;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return DSP_OK;
 }
 
 }  // namespace

@@ -398,15 +398,22 @@ class CrossModelKVMap:
     def map_into(self, k: torch.Tensor, v: torch.Tensor,
                  source_rope: tuple[torch.Tensor, torch.Tensor],
                  target_rope: tuple[torch.Tensor, torch.Tensor], cache, block_ids: list[int],
-                 use_residual: bool = True) -> None:
+                 use_residual: bool = True, prompt_len: int | None = None) -> None:
         """map() followed by cache.import_contiguous(block_ids, keys, values), with each
         target layer's GEMM writing its rows (keys re-rotated) straight into the cache's
         blocks: no (L_tgt, T, H, D) intermediate.  Layers whose map has no fused form (a
-        trained residual) take map's path for that layer and are then scattered."""
+        trained residual) take map's path for that layer and are then scattered.
+
+        With `prompt_len`, this is an admission (the target request's prompt has
+        prompt_len tokens): the T mapped tokens must cover at least one and fewer than
+        all of them, checked before any launch with the reference scheduler's message
+        (dispec/sched/scheduler.py:110-112)."""
+        L_src, T, H, D = k.shape
+        if prompt_len is not None:
+            check_prefix_coverage(T, prompt_len)
         _lib.require_gpu(k, v)
         if self.dtype != torch.bfloat16:
             raise ValueError("the HIP map runs bf16 maps (load with dtype=torch.bfloat16)")
-        L_src, T, H, D = k.shape
         if len(self.keys) != cache.num_layers or (cache.num_kv_heads, cache.head_dim) != (H, D):
             raise ValueError(f"a {len(self.keys)}-layer map of {H}x{D} heads cannot fill a "
                              f"{cache.num_layers}-layer cache of {cache.num_kv_heads}x"

@@ -32,6 +32,8 @@ from __future__ import annotations
 import ctypes
 import itertools
 import queue as _queue
+import time
+import weakref
 
 import torch
 
@@ -170,7 +172,9 @@ class HipIpcTransport(Transport):
         self._q = queue
         self._acks = acks
         self._inflight: dict[int, tuple] = {}   # sender: id -> regions kept alive
-        self._exported: dict[int, _DeviceMemory] = {}   # sender: data_ptr -> its region
+        # sender: data_ptr -> the exported region behind it, held weakly: the payload's
+        # tensors keep a region alive, so one exported and dropped unsent frees itself
+        self._exported: weakref.WeakValueDictionary = weakref.WeakValueDictionary()
         self._mapped: dict[int, int] = {}       # receiver: id(payload) -> message id
 
     @staticmethod
@@ -206,7 +210,7 @@ class HipIpcTransport(Transport):
         return KVPayload(list(tokens), k, v, dict(meta))
 
     def send(self, payload: KVPayload) -> None:
-        self._collect_acks(block=False)
+        self._collect_acks(timeout=None)
         msg_id = next(self._ids)
         keep, parts = [], {}
         for name, t in (("k", payload.k), ("v", payload.v)):
@@ -231,27 +235,38 @@ class HipIpcTransport(Transport):
     def send_sentinel(self) -> None:
         self._q.put(None)
 
-    def _collect_acks(self, block: bool) -> None:
+    def _collect_acks(self, timeout: float | None) -> None:
+        """Free the regions of acknowledged payloads: those already acknowledged when
+        timeout is None, otherwise waiting up to `timeout` seconds for all of them."""
         if self._acks is None:
             return
+        deadline = None if timeout is None else time.monotonic() + timeout
         while self._inflight:
             try:
-                msg_id = self._acks.get(block=block, timeout=None)
+                if deadline is None:
+                    msg_id = self._acks.get(block=False)
+                else:
+                    msg_id = self._acks.get(timeout=max(0.0, deadline - time.monotonic()))
             except _queue.Empty:
                 return
             self._inflight.pop(msg_id, None)
-            block = False
 
-    def release(self) -> None:
+    def release(self, timeout: float = 120.0) -> None:
         """Drop every sent payload's regions (reference semantics: call once the consumer
-        has mapped them; with acknowledgements this waits for the outstanding ones)."""
+        has mapped them).  With acknowledgements this waits up to `timeout` seconds for the
+        outstanding ones and raises TimeoutError, keeping the unacknowledged regions, if
+        the receiver has not answered by then (it may have died with the mappings open)."""
         if self._acks is not None:
-            self._collect_acks(block=True)
+            self._collect_acks(timeout=timeout)
+            if self._inflight:
+                raise TimeoutError(f"{len(self._inflight)} sent payloads still unacknowledged "
+                                   f"after {timeout:g} s; their regions are kept until "
+                                   "release() succeeds or this transport is dropped")
         self._inflight.clear()
 
     @property
     def in_flight(self) -> int:
-        self._collect_acks(block=False)
+        self._collect_acks(timeout=None)
         return len(self._inflight)
 
     # -- receiving side -------------------------------------------------------------------

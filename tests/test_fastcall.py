@@ -24,6 +24,25 @@ def test_fast_names_are_bound_to_the_fast_module():
 
 
 @pytest.mark.parametrize("name", _lib.FAST_CALLS)
+def test_fast_signatures_equal_the_ctypes_argtypes(name):
+    """The type letters the fast module converts each argument with are the ctypes
+    argtypes of the same entry point, position by position (an int32 / int64 swap at any
+    position would otherwise reach the kernels as a wrong value)."""
+    assert FAST.SIGNATURES[name] == _lib.type_letters(_lib.SIGNATURES[name][1])
+    assert name in _lib.calls().fast_bound
+
+
+def test_a_stale_fast_signature_falls_back_to_ctypes(monkeypatch):
+    name = "dsp_kv_append"
+    sig = FAST.SIGNATURES[name]
+    monkeypatch.setitem(FAST.SIGNATURES, name, sig[:8] + ("i" if sig[8] == "q" else "q") + sig[9:])
+    calls = _lib._Calls(_lib.lib())
+    assert name not in calls.fast_bound
+    assert isinstance(getattr(calls, name), ctypes._CFuncPtr)
+    assert getattr(calls, "dsp_paged_decode") is FAST.dsp_paged_decode
+
+
+@pytest.mark.parametrize("name", _lib.FAST_CALLS)
 def test_wrong_argument_count_and_type_raise(name):
     fn = getattr(_lib.calls(), name)
     n = len(_lib.SIGNATURES[name][1])
