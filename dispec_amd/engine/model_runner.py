@@ -19,8 +19,13 @@ the HF modules, unchanged.  What the backend replaces is the KV path inside `_at
                                         prefix-cache hits) the shared-prefix variant
                                         attends those blocks once for the whole batch
 
-Only "hip" is accepted: the reference's "native"/"triton" backends are torch/Triton
-code paths this package does not carry.
+attn_backend is a string switch as in the reference (:48-52): "hip" (the default here)
+runs the kernels above; "native" keeps the reference's torch attention -- per sequence, the
+context gathered from the pool (by the slot-gather kernel) and torch's SDPA with the
+bottom-right causal mask and grouped heads (:160-185) -- on the same projections, prologue
+and cache, as the baseline a deployment can switch back to.  "triton" names the
+reference's Triton decode kernel, which this package does not carry: it is refused with a
+message pointing at "hip", its replacement.
 """
 
 from __future__ import annotations
@@ -60,39 +65,62 @@ class _Batch:
     workspace: torch.Tensor | None = None
     shared_prefix: int = 0   # leading context tokens all sequences share (0: none used)
     balanced: bool = False   # short query blocks on the balanced split-K kernel
+    seqs: tuple = ()         # the host SeqMeta list (attn_backend="native" walks it)
+
+
+_BACKENDS = ("hip", "native")
+
+
+def _compute_dtype(model) -> torch.dtype:
+    """The model's arithmetic type: its first floating-point parameter's (quantised models
+    keep integer-packed weights beside float scales)."""
+    for p in model.parameters():
+        if p.is_floating_point():
+            return p.dtype
+    return torch.float16
+
+
+@dataclass(frozen=True)
+class _FusedLayer:
+    """One layer's projections concatenated for one GEMM each (fuse=True)."""
+
+    qkv_weight: torch.Tensor              # rows: q heads, then k heads, then v heads
+    qkv_bias: torch.Tensor | None
+    gate_up_weight: torch.Tensor          # rows: gate, then up
 
 
 class ModelRunner:
     def __init__(self, model, attn_backend: str = "hip", fuse: bool = False):
-        if attn_backend != "hip":
-            raise ValueError(f"attn_backend {attn_backend!r}: dispec_amd runs attention on its "
-                             "HIP kernels only (attn_backend='hip')")
-        self.model = model
-        self.attn_backend = attn_backend
-        cfg = model.config
-        self.cfg = cfg
+        if attn_backend not in _BACKENDS:
+            hint = (" (the Triton decode kernel is replaced by this package's HIP kernels: "
+                    "use attn_backend='hip')" if attn_backend == "triton" else "")
+            raise ValueError(f"attn_backend {attn_backend!r} is not one of {_BACKENDS}{hint}")
+        self.model, self.attn_backend = model, attn_backend
+        self.cfg = cfg = model.config
+        self.dtype = _compute_dtype(model)
         self.device = next(model.parameters()).device
-        self.dtype = next((p.dtype for p in model.parameters() if p.is_floating_point()),
-                          torch.float16)
-        core = model.model
-        self.embed, self.layers, self.norm = core.embed_tokens, core.layers, core.norm
+        backbone = model.model
+        self.embed = backbone.embed_tokens
+        self.layers = backbone.layers
+        self.norm = backbone.norm
+        self.rotary_emb = backbone.rotary_emb    # the model's own cos/sin tables
         self.lm_head = model.lm_head
         self.num_heads = cfg.num_attention_heads
         self.num_kv_heads = cfg.num_key_value_heads
-        self.head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        self.head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // self.num_heads
         self.kv_groups = self.num_heads // self.num_kv_heads
-        self.scale = self.head_dim ** -0.5
+        self.scale = 1.0 / self.head_dim ** 0.5
+        if "sliding_attention" in (getattr(cfg, "layer_types", None) or ()):
+            raise ValueError(f"{type(model).__name__} uses sliding-window attention layers, which "
+                             "the paged attention path does not implement")
+        first = self.layers[0].self_attn
+        self.qk_norm = all(hasattr(first, n) for n in ("q_norm", "k_norm"))   # Qwen3
         # the MFMA attention kernels (and with them the balanced verify split and the shared
         # prefix) serve bf16 / fp16; fp32 models attend through the generic kernel
         self._tuned_attention = self.dtype in (torch.bfloat16, torch.float16)
-        attn0 = self.layers[0].self_attn
-        self.qk_norm = hasattr(attn0, "q_norm") and hasattr(attn0, "k_norm")
-        if "sliding_attention" in (getattr(cfg, "layer_types", None) or []):
-            raise ValueError(f"{type(model).__name__} uses sliding-window attention layers, which "
-                             "the paged attention path does not implement")
-        self.rotary_emb = core.rotary_emb
         self._rope_dummy = torch.zeros(1, 1, device=self.device, dtype=self.dtype)
-        self.fused = self._build_fused() if fuse else False
+        self._fused: list[_FusedLayer] = self._fuse_projections() if fuse else []
+        self.fused = bool(self._fused)
         # shared-prefix attention: used when at least this many sequences share at least
         # this many leading tokens (fewer gain nothing over per-sequence attention)
         self.shared_prefix_min_seqs = 4
@@ -103,26 +131,31 @@ class ModelRunner:
         self._cus = (torch.cuda.get_device_properties(self.device).multi_processor_count
                      if self.device.type == "cuda" else 256)
 
-    def _build_fused(self) -> bool:
-        """One GEMM for q/k/v and one for gate/up per layer (model_runner.py:93-118)."""
-        a0 = self.layers[0].self_attn
-        if isinstance(a0.q_proj, nn.Identity):
+    def _fuse_projections(self) -> list[_FusedLayer]:
+        """fuse=True (model_runner.py:93-118): per layer, q/k/v become one GEMM and gate/up
+        another; the separate projection modules are replaced by nn.Identity, so the model
+        is changed in place and serves one fused runner.  Quantised projections (not float
+        nn.Linear) are left as they are: returns [] and the runner stays unfused."""
+        probe = self.layers[0].self_attn.q_proj
+        if isinstance(probe, nn.Identity):
             raise ValueError("model already fused by another ModelRunner; fuse=True mutates "
                              "the model in place -- use one fused runner per model instance")
-        if not (isinstance(a0.q_proj, nn.Linear) and a0.q_proj.weight.is_floating_point()):
-            return False
-        self._qkv_w, self._qkv_b, self._gate_up_w = [], [], []
+        if not isinstance(probe, nn.Linear) or not probe.weight.is_floating_point():
+            return []
+        fused = []
         for layer in self.layers:
-            a, m = layer.self_attn, layer.mlp
-            self._qkv_w.append(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0))
-            self._qkv_b.append(torch.cat([a.q_proj.bias, a.k_proj.bias, a.v_proj.bias], 0)
-                               if a.q_proj.bias is not None else None)
-            self._gate_up_w.append(torch.cat([m.gate_proj.weight, m.up_proj.weight], 0))
-            a.q_proj = a.k_proj = a.v_proj = nn.Identity()
-            m.gate_proj = m.up_proj = nn.Identity()
-        self._qsz = self.num_heads * self.head_dim
-        self._kvsz = self.num_kv_heads * self.head_dim
-        return True
+            attn, mlp = layer.self_attn, layer.mlp
+            projs = (attn.q_proj, attn.k_proj, attn.v_proj)
+            biases = [p.bias for p in projs]
+            fused.append(_FusedLayer(
+                qkv_weight=torch.cat([p.weight for p in projs]),
+                qkv_bias=None if biases[0] is None else torch.cat(biases),
+                gate_up_weight=torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight])))
+            for name in ("q_proj", "k_proj", "v_proj"):
+                setattr(attn, name, nn.Identity())
+            for name in ("gate_proj", "up_proj"):
+                setattr(mlp, name, nn.Identity())
+        return fused
 
     def rope(self, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         cos, sin = self.rotary_emb(self._rope_dummy, positions[None, :])
@@ -153,7 +186,8 @@ class ModelRunner:
                     self._prefer_balanced(seq_meta, max_q_len, max_ctx, cache.block_size))
         return _Batch(block_table=dev[2 * B + 1:].view(B, width), ctx_lens=dev[:B],
                       cu_q=dev[B:2 * B + 1], max_q_len=max_q_len, max_ctx=max_ctx,
-                      decode=decode, shared_prefix=shared, balanced=balanced)
+                      decode=decode, shared_prefix=shared, balanced=balanced,
+                      seqs=tuple(seq_meta))
 
     def _prefer_balanced(self, seq_meta: list[SeqMeta], max_q_len: int, max_ctx: int,
                          bs: int) -> bool:
@@ -191,24 +225,27 @@ class ModelRunner:
         return tokens if tokens >= self.shared_prefix_min_tokens else 0
 
     # -- attention for one layer --------------------------------------------------------
+    def _project_qkv(self, attn, x: torch.Tensor, layer_idx: int):
+        """q (T, Hq, D), k and v (T, KVH, D) of one layer; with fuse=True, views of one
+        GEMM's output (heads laid out q, then k, then v, each row-strided)."""
+        heads = (self.num_heads, self.num_kv_heads, self.num_kv_heads)
+        if self._fused:
+            f = self._fused[layer_idx]
+            qkv = F.linear(x, f.qkv_weight, f.qkv_bias).unflatten(-1, (-1, self.head_dim))
+            return qkv.split(heads, dim=1)
+        projs = (attn.q_proj, attn.k_proj, attn.v_proj)
+        return tuple(p(x).unflatten(-1, (n, self.head_dim)) for p, n in zip(projs, heads))
+
     def _attention(self, layer, x, cos, sin, write_slots, cache, layer_idx, batch: _Batch):
         attn = layer.self_attn
-        T = x.shape[0]
-        if self.fused:
-            qkv = F.linear(x, self._qkv_w[layer_idx], self._qkv_b[layer_idx])
-            q, k, v = qkv.split([self._qsz, self._kvsz, self._kvsz], dim=-1)
-            q = q.view(T, self.num_heads, self.head_dim)
-            k = k.view(T, self.num_kv_heads, self.head_dim)
-            v = v.view(T, self.num_kv_heads, self.head_dim)
-        else:
-            q = attn.q_proj(x).view(T, self.num_heads, self.head_dim)
-            k = attn.k_proj(x).view(T, self.num_kv_heads, self.head_dim)
-            v = attn.v_proj(x).view(T, self.num_kv_heads, self.head_dim)
+        q, k, v = self._project_qkv(attn, x, layer_idx)
         # q_norm / k_norm (Qwen3), RoPE on q and k, and cache.write(k, v): one launch
         q = qk_norm_rope_append(q, k, v, cos, sin, write_slots, cache, layer_idx,
                                 attn.q_norm if self.qk_norm else None,
                                 attn.k_norm if self.qk_norm else None)
-        if batch.decode and not batch.shared_prefix:
+        if self.attn_backend == "native":
+            o = self._torch_attention(q, cache, layer_idx, batch.seqs)
+        elif batch.decode and not batch.shared_prefix:
             o = paged_decode_attention_blocks(
                 q, cache.key[layer_idx], cache.value[layer_idx], batch.block_table,
                 batch.ctx_lens, self.kv_groups, block_size=cache.block_size, scale=self.scale,
@@ -219,7 +256,30 @@ class ModelRunner:
                 batch.ctx_lens, self.kv_groups, block_size=cache.block_size, scale=self.scale,
                 max_q_len=batch.max_q_len, max_ctx=batch.max_ctx, workspace=batch.workspace,
                 shared_prefix_tokens=batch.shared_prefix, balanced=batch.balanced)
-        return attn.o_proj(o.reshape(T, self.num_heads * self.head_dim))
+        return attn.o_proj(o.flatten(1))
+
+    def _torch_attention(self, q: torch.Tensor, cache: PagedKVCache, layer_idx: int,
+                         seqs) -> torch.Tensor:
+        """attn_backend="native": the reference's per-sequence attention
+        (model_runner.py:160-185) -- the sequence's context rows gathered from the pool
+        (the prologue has already appended this step's k and v, so a fresh prefill reads
+        back exactly the rows it projected), then torch SDPA with the bottom-right causal
+        mask and grouped KV heads.  SDPA runs in float32: torch's bf16 batched matmul on
+        the transposed key operand SDPA forms is avoided on this platform; the output is
+        rounded to the model dtype."""
+        from torch.nn.attention.bias import causal_lower_right
+        out = torch.empty_like(q)
+        end = 0
+        for m in seqs:
+            start, end = end, end + m.q_len
+            keys, vals = cache.gather(layer_idx, cache.context_slots(m.block_ids, m.ctx_len))
+            as_bhd = lambda t: t.float().transpose(0, 1).unsqueeze(0)  # noqa: E731
+            o = F.scaled_dot_product_attention(
+                as_bhd(q[start:end]), as_bhd(keys), as_bhd(vals),
+                attn_mask=causal_lower_right(m.q_len, m.ctx_len), scale=self.scale,
+                enable_gqa=True)
+            out[start:end] = o[0].transpose(0, 1)
+        return out
 
     @torch.inference_mode()
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor,
@@ -239,7 +299,7 @@ class ModelRunner:
         multi-query kernel, which reads those blocks once for the batch."""
         cos, sin = self.rope(positions)
         x = self.embed(token_ids)
-        if batch.workspace is None:
+        if batch.workspace is None and self.attn_backend == "hip":
             B = batch.ctx_lens.shape[0]
             if batch.decode and not batch.shared_prefix:
                 batch.workspace = decode_workspace(B, self.num_heads, self.num_kv_heads,
@@ -258,12 +318,12 @@ class ModelRunner:
         return self.norm(x)
 
     def _mlp(self, layer, h, i):
-        if not self.fused:
-            return layer.mlp(h)
-        gate, up = F.linear(h, self._gate_up_w[i]).chunk(2, dim=-1)
-        return layer.mlp.down_proj(layer.mlp.act_fn(gate) * up)
+        mlp = layer.mlp
+        if not self._fused:
+            return mlp(h)
+        gate_up = F.linear(h, self._fused[i].gate_up_weight).unflatten(-1, (2, -1))
+        return mlp.down_proj(mlp.act_fn(gate_up[..., 0, :]) * gate_up[..., 1, :])
 
     def logits(self, hidden: torch.Tensor, indices: torch.Tensor | None = None) -> torch.Tensor:
-        if indices is not None:
-            hidden = hidden[indices]
-        return self.lm_head(hidden)
+        """lm_head over the hidden states (of the rows `indices` selects, when given)."""
+        return self.lm_head(hidden if indices is None else hidden[indices])

@@ -30,10 +30,11 @@ def _pair(family, dtype=torch.bfloat16):
 class _Both:
     """Drive the HIP runner and the CPU oracle through identical cache operations."""
 
-    def __init__(self, gpu_model, cpu_model, num_blocks=64, bs=16, dtype=torch.bfloat16):
+    def __init__(self, gpu_model, cpu_model, num_blocks=64, bs=16, dtype=torch.bfloat16,
+                 backend="hip", fuse=False):
         from dispec_amd.engine.model_runner import ModelRunner
         from dispec_amd.kv.paged_cache import PagedKVCache
-        self.runner = ModelRunner(gpu_model, attn_backend="hip")
+        self.runner = ModelRunner(gpu_model, attn_backend=backend, fuse=fuse)
         self.cache = PagedKVCache.for_model(gpu_model.config, num_blocks, bs, dtype, DEV)
         cfg = cpu_model.config
         shape = (cfg.num_hidden_layers, num_blocks * bs, cfg.num_key_value_heads, cfg.head_dim)
@@ -210,7 +211,25 @@ def test_verify_of_skewed_sequences_uses_the_balanced_split(family):
     assert batch.balanced and not batch.shared_prefix and not batch.decode
 
 
-def test_rejects_other_backends():
-    from dispec_amd.engine.model_runner import ModelRunner
-    with pytest.raises(ValueError, match="hip"):
-        ModelRunner(toy_lm("qwen3"), attn_backend="triton")
+@pytest.mark.parametrize("backend,fuse", [("native", False), ("native", True), ("hip", True)])
+@pytest.mark.parametrize("family", sorted(FAMILIES))
+def test_other_backend_and_fused_projections(family, backend, fuse):
+    """attn_backend="native" (the reference's per-sequence torch SDPA over the gathered
+    context, kept as a peer of "hip") and fuse=True (one GEMM for q/k/v and one for
+    gate/up, model_runner.py:93-118) against the oracle's native forward: a prefill, 12
+    decode steps across a block boundary, and a decode row beside a fresh prefill."""
+    gm, cm = _pair(family)
+    both = _Both(gm, cm, backend=backend, fuse=fuse)
+    assert both.runner.fused == fuse and both.runner.attn_backend == backend
+    ids = torch.randint(0, 128, (27,), generator=torch.Generator().manual_seed(18)).tolist()
+    got, ref = both.forward([(1, ids, 0)])
+    assert _cos(got, ref).min() >= 0.999
+    nxt, cur = int(ref[-1].argmax()), len(ids)
+    for step in range(12):
+        got, ref = both.forward([(1, [nxt], cur)])
+        c = _cos(got[0], ref[0]).item()
+        assert c >= 0.999, f"{backend} fuse={fuse} step {step}: cosine {c:.5f}"
+        nxt, cur = int(ref[0].argmax()), cur + 1
+    b = torch.randint(0, 128, (11,), generator=torch.Generator().manual_seed(19)).tolist()
+    got, ref = both.forward([(1, [nxt], cur), (2, b, 0)])
+    assert _cos(got, ref).min() >= 0.999
