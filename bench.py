@@ -69,15 +69,15 @@ _PROBE = None
 
 
 def _probe_lib():
-    """libdispec_probe.so: the bandwidth probes (dispec_amd/probe/dsp_probe.h), built beside
-    the product library but not part of it."""
+    """libdispec_probe.so: the bandwidth probes (bench_probes/dsp_probe.h), measurement
+    instruments built beside the product library but not part of it."""
     global _PROBE
     if _PROBE is None:
         import ctypes
         from ctypes import c_int, c_int32, c_int64, c_void_p
-        path = os.path.join(ROOT, "dispec_amd", "libdispec_probe.so")
+        path = os.path.join(ROOT, "bench_probes", "libdispec_probe.so")
         if not os.path.exists(path):
-            raise RuntimeError(f"{path} is not built; run `python -m dispec_amd.build` first")
+            raise RuntimeError(f"{path} is not built; run `python -m bench_probes.build` first")
         lib = ctypes.CDLL(path)
         P = c_void_p
         sigs = {"dsp_probe_stream_read": [P, c_int64, c_int32, P, P],

@@ -13,7 +13,7 @@
 extern "C" {
 #endif
 
-#include "../../include/dispec_hip.h" /* dsp_stream_t, DSP_E* */
+#include "../include/dispec_hip.h" /* dsp_stream_t, DSP_E* */
 
 /* Probes with no counterpart in the reference.  Each returns 0, a negative DSP_E* status
  * of dispec_hip.h for an invalid argument (nothing launched), or a positive hipError_t.

@@ -7,7 +7,7 @@
 // every 2 KiB slot row) caps what the decode can fetch below a streaming read.  Both probes
 // reduce what they read to one word that is stored only if it matches a sentinel, so the
 // loads cannot be removed.
-#include "../csrc/dsp_common.h"
+#include "../dispec_amd/csrc/dsp_common.h"
 #include "dsp_probe.h"
 
 namespace {

@@ -1,9 +1,9 @@
 """Build libdispec_hip.so from dispec_amd/csrc/*.hip for gfx950 with hipcc.
 
 Every source is compiled to an object in dispec_amd/_build/ (in parallel), then linked
-into dispec_amd/libdispec_hip.so in-tree, where the loader looks for it.  The bandwidth
-probes of dispec_amd/probe/ go into a separate libdispec_probe.so that only bench.py
-loads.  Run as `python -m dispec_amd.build`.
+into dispec_amd/libdispec_hip.so in-tree, where the loader looks for it, and the fast
+binding csrc/fastcall.c into the dispec_amd._fastcall module.  Run as
+`python -m dispec_amd.build`.
 """
 
 from __future__ import annotations
@@ -19,9 +19,6 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ_DIR = PKG / "_build"
 LIB = PKG / "libdispec_hip.so"
-# measurement-only kernels (bench.py's bandwidth probes), kept out of the product library
-PROBE_SRC = PKG / "probe"
-PROBE_LIB = PKG / "libdispec_probe.so"
 ARCH = os.environ.get("DISPEC_HIP_ARCH", "gfx950")
 
 # Packed-fp32 VALU ops are switched off for all device code: hipcc would otherwise form
@@ -41,8 +38,8 @@ def _hipcc() -> str:
     return path
 
 
-def _compile(src: Path, verbose: bool) -> Path:
-    obj = OBJ_DIR / (src.stem + ".o")
+def _compile(src: Path, verbose: bool, obj_dir: Path = OBJ_DIR) -> Path:
+    obj = obj_dir / (src.stem + ".o")
     cmd = [_hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
@@ -82,21 +79,17 @@ def _build_fastcall(verbose: bool) -> Path:
 
 
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every csrc/*.hip into libdispec_hip.so (the product library), every
-    probe/*.hip into libdispec_probe.so (bench-side) and csrc/fastcall.c into the
-    dispec_amd._fastcall module.  Returns the product library path."""
+    """Compile every csrc/*.hip into libdispec_hip.so (the product library) and
+    csrc/fastcall.c into the dispec_amd._fastcall module.  Returns the library path."""
     sources = sorted(CSRC.glob("*.hip"))
-    probes = sorted(PROBE_SRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     OBJ_DIR.mkdir(exist_ok=True)
-    jobs = jobs or min(len(sources) + len(probes), max(1, (os.cpu_count() or 2)))
+    jobs = jobs or min(len(sources), max(1, (os.cpu_count() or 2)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile(s, verbose), sources + probes))
-    if probes:
-        _link(objs[len(sources):], PROBE_LIB, verbose)
+        objs = list(pool.map(lambda s: _compile(s, verbose), sources))
     _build_fastcall(verbose)
-    return _link(objs[:len(sources)], LIB, verbose)
+    return _link(objs, LIB, verbose)
 
 
 if __name__ == "__main__":

@@ -15,7 +15,14 @@
  *     row of num_kv_heads*head_dim contiguous elements (paged_cache.py:3-7, :39).
  *   - Nothing here allocates device memory or synchronises the host: outputs and the
  *     split-K workspace are passed in by the caller, and all work is enqueued on
- *     `stream`.  The library holds no mutable global state.
+ *     `stream`.  Device-side global state is limited to (a) two write-only 4 KiB sink
+ *     regions (the append and the attention prologue send the stores of a skipped row
+ *     there instead of branching around them; nothing ever reads them, so concurrent
+ *     calls stay independent) and (b) the 32 MiB scratch array of
+ *     dsp_paged_decode_noalloc, shared by every call of that one entry point on a
+ *     device (overlapping calls of it race; every other entry point is reentrant
+ *     across streams).  Host-side, the library keeps only that array's per-device
+ *     address once looked up.
  *   - Return value: 0 on success, a negative DSP_E* code for an invalid argument
  *     (nothing was launched), or a positive hipError_t from the launch.
  *   - `err_count` (optional, may be NULL) is a device int32 that the kernels
