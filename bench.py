@@ -369,11 +369,24 @@ def bench_c2(torch) -> dict:
 
     step_s = _time_gpu(torch, step, 5)
     dec_s = _time_gpu(torch, decode_only, 5) / L
+    # the append at bandwidth scale (BASELINE's append row): every sequence's whole
+    # context written as a prefill would write it, through the same block tables -- runs
+    # of 16 consecutive slots per randomly placed block -- one launch for the layer
+    cslots = torch.cat([cache.context_slots(t, int(n)) for t, n in zip(tables, ctx)])
+    n_rows = cslots.numel()
+    kp = torch.randn((n_rows, KVH, D), generator=g, device=dev).to(torch.bfloat16)
+    vp = torch.randn((n_rows, KVH, D), generator=g, device=dev).to(torch.bfloat16)
+    app_s = _time_gpu_cold(torch, lambda: cache.write(5, cslots, kp, vp), 20)
+    app_warm_s = _time_gpu(torch, lambda: cache.write(5, cslots, kp, vp), 20)
     cache.check_errors()
     kv_bytes = int(ctx.sum()) * KVH * D * 2 * 2
+    app_bytes = 2 * 2 * n_rows * cache.row_bytes
     res = {"c2_step_us_per_layer": step_s / L * 1e6, "c2_decode_us_per_layer": dec_s * 1e6,
-           "c2_decode_GBps": kv_bytes / dec_s / 1e9}
-    del cache
+           "c2_decode_GBps": kv_bytes / dec_s / 1e9,
+           "c2_append_prefill_rows": n_rows, "c2_append_prefill_us": app_s * 1e6,
+           "c2_append_prefill_GBps": app_bytes / app_s / 1e9,
+           "c2_append_prefill_warm_GBps": app_bytes / app_warm_s / 1e9}
+    del cache, kp, vp
     torch.cuda.empty_cache()
     return res
 
@@ -624,7 +637,10 @@ def bench_c4(torch) -> dict:
                            20)
     cow_warm_s = _time_gpu(torch, lambda: cache.copy_block_fanout_device(cache, fork_src, dst),
                            20)
-    cow_bytes = 2 * 2 * L * len(pairs) * cache.block_bytes
+    # HBM bytes the fork moves: each copy's block written, the source block read once per
+    # group of 8 copies (the fan-out kernel loads a piece once and stores it 8 times)
+    fan = 8
+    cow_hbm_bytes = 2 * L * cache.block_bytes * (len(pairs) + -(-len(pairs) // fan))
     # suffix + draft tokens: one append per layer for all 32 sequences
     rows, wslots = [], []
     for s in range(S):
@@ -695,8 +711,9 @@ def bench_c4(torch) -> dict:
     cache.check_errors()
     spill.check_errors()
     res = {
-        "c4_cow_pairs": len(pairs), "c4_cow_us": cow_s * 1e6, "c4_cow_GBps": cow_bytes / cow_s / 1e9,
-        "c4_cow_warm_GBps": cow_bytes / cow_warm_s / 1e9,
+        "c4_cow_pairs": len(pairs), "c4_cow_us": cow_s * 1e6, "c4_cow_hbm_bytes": cow_hbm_bytes,
+        "c4_cow_GBps": cow_hbm_bytes / cow_s / 1e9,
+        "c4_cow_warm_GBps": cow_hbm_bytes / cow_warm_s / 1e9,
         "c4_append_rows": n, "c4_append_GBps": 2 * 2 * n * cache.row_bytes / app_s / 1e9,
         "c4_append_warm_GBps": 2 * 2 * n * cache.row_bytes / app_warm_s / 1e9,
         "c4_verify_us_per_layer": ver_s * 1e6,
@@ -898,6 +915,11 @@ def bench_c5(torch) -> dict:
                                              sink.data_ptr(), stream), "probe")
     w_probe = torch.empty((kv, kv), dtype=torch.bfloat16, device=dev).normal_()
     fill_s = _time_gpu(torch, fill_probe, 20)
+    # the vendor library on the same problem size (hipBLASLt through torch.matmul): one
+    # (8 x 4096, 1024) x (1024, 1024) bf16 product, both operands contiguous
+    x_lib = kbuf[:R * T].view(R * T, kv)
+    w_lib = w_probe.contiguous()
+    lib_s = _time_gpu(torch, lambda: torch.matmul(x_lib, w_lib), 20)
     # scatter into a 36-layer target pool
     tgt = PagedKVCache(Lt, NB, bs, KVH, D, device=dev)
     perm = torch.randperm(NB, generator=gcpu)[:nb].view(R, T // bs)
@@ -944,6 +966,7 @@ def bench_c5(torch) -> dict:
     per_launch = m_s / (2 * len(maps))
     res["c5_map_fill_floor_us"] = round(fill_s * 1e6, 2)
     res["c5_map_us_per_launch"] = round(per_launch * 1e6, 2)
+    res["c5_map_hipblaslt_us"] = round(lib_s * 1e6, 2)
     res["c5_map_roofline"] = {
         "bound": "mfma", "achieved": round(flops / m_s / 1e12, 1), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(flops / m_s / 1e12 / PEAK_BF16_TFLOPS, 4),
