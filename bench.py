@@ -87,6 +87,9 @@ def _probe_lib():
                 "dsp_probe_gemm_fill": [P, c_int64, c_int64, c_int64, P, c_int64, c_int64,
                                         c_int64, c_int32, P, P],
                 "dsp_probe_piece_scatter": [P, P, c_int64, c_int64, P, P],
+                "dsp_probe_piece_gather": [P, P, c_int64, c_int64, P, P],
+                "dsp_probe_batch_read": [P, P, c_int64, P, c_int64, c_int32, P, P, c_int32,
+                                         c_int32, P, P],
                 "dsp_probe_piece_fill": [P, c_int64, c_int64, P, P]}
         for name, args in sigs.items():
             fn = getattr(lib, name)
@@ -327,6 +330,7 @@ def _cpu_model() -> str:
 def bench_c2(torch) -> dict:
     """Qwen2.5-1.5B decode step: 28 layers, Hq 12, KVH 2, D 128, B 64, ctx ~U[512, 4096],
     blocks scattered over a pool of 1.25x the tokens; per layer append + decode."""
+    from dispec_amd import _lib
     from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
     from dispec_amd.kv.paged_cache import PagedKVCache
 
@@ -370,6 +374,22 @@ def bench_c2(torch) -> dict:
 
     step_s = _time_gpu(torch, step, 5)
     dec_s = _time_gpu(torch, decode_only, 5) / L
+    # the floor of the decode: the same layers' K/V read with no arithmetic, every
+    # sequence cut into equal 256-key pieces (dsp_probe_batch_read), same 28-layer loop
+    work = torch.tensor([[b, k0] for b, n in enumerate(ctx.tolist()) for k0 in range(0, n, 256)],
+                        dtype=torch.int32).to(dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    probe = _probe_lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def read_only():
+        for layer in range(L):
+            _lib.check(probe.dsp_probe_batch_read(
+                cache.key[layer].data_ptr(), cache.value[layer].data_ptr(), cache.num_slots,
+                bt.data_ptr(), bt.stride(0), bs, ctx_lens.data_ptr(), work.data_ptr(),
+                work.shape[0], KVH, sink.data_ptr(), stream), "probe")
+
+    floor_s = _time_gpu(torch, read_only, 5) / L
     # the append at bandwidth scale (BASELINE's append row): every sequence's whole
     # context written as a prefill would write it, through the same block tables -- runs
     # of 16 consecutive slots per randomly placed block -- one launch for the layer
@@ -384,6 +404,8 @@ def bench_c2(torch) -> dict:
     app_bytes = 2 * 2 * n_rows * cache.row_bytes
     res = {"c2_step_us_per_layer": step_s / L * 1e6, "c2_decode_us_per_layer": dec_s * 1e6,
            "c2_decode_GBps": kv_bytes / dec_s / 1e9,
+           "c2_read_floor_us_per_layer": floor_s * 1e6,
+           "c2_read_floor_GBps": kv_bytes / floor_s / 1e9,
            "c2_append_prefill_rows": n_rows, "c2_append_prefill_us": app_s * 1e6,
            "c2_append_prefill_GBps": app_bytes / app_s / 1e9,
            "c2_append_prefill_warm_GBps": app_bytes / app_warm_s / 1e9}
@@ -993,9 +1015,11 @@ def bench_copy_ceiling(torch) -> dict:
     """The ceiling of the byte-moving kernels on this GPU: a 2 GiB streaming copy
     (dsp_probe_stream_copy, non-temporal loads and stores), best of three grid sizes --
     64, 16 and 4 KiB per workgroup, the last two one-shot workgroups -- read + write bytes
-    over time; and the same copy with its destinations permuted in 32 KiB blocks and in
-    2 KiB rows (dsp_probe_piece_scatter), the write patterns of scatter / block copy and of
-    the append; and stores alone, in order and to random 32 KiB blocks (dsp_probe_piece_fill,
+    over time; and the same copy with its destinations permuted in 32 KiB blocks, 8 KiB
+    blocks and 2 KiB rows (dsp_probe_piece_scatter), the write patterns of scatter / block
+    copy, of config 2's prefill-scale append (8 KiB blocks) and of a random-slot append; the
+    copy with its sources permuted in 32 KiB blocks (dsp_probe_piece_gather), the transport
+    gather's pattern; and stores alone, in order and to random 32 KiB blocks (dsp_probe_piece_fill,
     bytes written over time: the copy-on-write fork reads its one source block from L2 and
     only writes HBM)."""
     from dispec_amd import _lib
@@ -1018,7 +1042,7 @@ def bench_copy_ceiling(torch) -> dict:
     # kernel with the identity permutation, the control
     g = torch.Generator(device="cuda").manual_seed(9)
     for name, piece, rand in (("inorder32k", 32768, False), ("block32k", 32768, True),
-                              ("row2k", 2048, True)):
+                              ("block8k", 8192, True), ("row2k", 2048, True)):
         perm = (torch.randperm(n // piece, generator=g, device="cuda") if rand else
                 torch.arange(n // piece, device="cuda")).to(torch.int32)
 
@@ -1032,6 +1056,12 @@ def bench_copy_ceiling(torch) -> dict:
                 _lib.check(lib.dsp_probe_piece_fill(dst.data_ptr(), n, piece, perm.data_ptr(),
                                                     stream), "probe")
             res[f"write_only_{name}_GBps"] = n / _time_gpu(torch, fill, 10) / 1e9
+        if name == "block32k":
+            # the same copy read from random 32 KiB blocks and written in order (the gather)
+            def gather():
+                _lib.check(lib.dsp_probe_piece_gather(src.data_ptr(), dst.data_ptr(), n, piece,
+                                                      perm.data_ptr(), stream), "probe")
+            res["gather_block32k_ceiling_GBps"] = 2 * n / _time_gpu(torch, gather, 10) / 1e9
         del perm
     del src, dst
     torch.cuda.empty_cache()

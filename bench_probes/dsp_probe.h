@@ -48,6 +48,19 @@ int dsp_probe_gemm_fill(const void* a, int64_t lda, int64_t M, int64_t a_batch_s
  *     random 32 KiB blocks (scatter, block copy) or 2 KiB rows (append). */
 int dsp_probe_piece_scatter(const void* src, void* dst, int64_t bytes, int64_t piece_bytes,
                             const int32_t* dst_index, dsp_stream_t stream);
+/*   dsp_probe_piece_gather: the opposite direction -- piece i of dst (contiguous) read from
+ *     src + src_index[i] * piece_bytes (piece_bytes a multiple of 4096 dividing bytes): the
+ *     ceiling of reads from random 32 KiB blocks written in order (the transport gather). */
+int dsp_probe_piece_gather(const void* src, void* dst, int64_t bytes, int64_t piece_bytes,
+                           const int32_t* src_index, dsp_stream_t stream);
+/*   dsp_probe_batch_read: the K/V read of a decode batch (head_dim 128, KVH <= 8) with no
+ *     arithmetic and equal work per workgroup: workgroup w reads keys [k0, min(k0 + 256,
+ *     ctx_lens[b])) of sequence b for all KV heads, (b, k0) = work[2w], work[2w + 1]; the
+ *     floor of a decode's time on those contexts. */
+int dsp_probe_batch_read(const void* k_cache, const void* v_cache, int64_t num_slots,
+                         const int32_t* block_table, int64_t bt_stride, int32_t block_size,
+                         const int32_t* ctx_lens, const int32_t* work, int32_t num_work,
+                         int32_t KVH, uint32_t* sink, dsp_stream_t stream);
 /*   dsp_probe_piece_fill: stores only -- fill `bytes` of dst (pieces of piece_bytes, a
  *     multiple of 4096 dividing bytes) with a constant, piece i at dst + dst_index[i] *
  *     piece_bytes: HBM write bandwidth in order (identity) or to random 32 KiB blocks. */

@@ -120,6 +120,62 @@ __global__ __launch_bounds__(256) void piece_scatter_kernel(const dsp_u32x4* __r
   dsp_st_stream(dsp_ld_stream(src + f), dst + int64_t(dst_index[i]) * piece16 + (f - i * piece16));
 }
 
+// The gather direction of the copy above: piece i of dst (contiguous) is read from
+// src + src_index[i] * piece_bytes -- random source blocks, contiguous writes, the access
+// pattern of the transport gather with no table logic.  Pieces of 4 KiB or more (one index
+// per workgroup).
+__global__ __launch_bounds__(256) void piece_gather_kernel(const dsp_u32x4* __restrict__ src,
+                                                           dsp_u32x4* __restrict__ dst,
+                                                           int64_t piece16, int64_t n16,
+                                                           const int32_t* __restrict__ src_index) {
+  const int64_t base = int64_t(blockIdx.x) * 256;
+  const int64_t f = base + threadIdx.x;
+  const int64_t i = base / piece16;  // uniform: the workgroup lies in one piece
+  const int64_t s = int64_t(src_index[i]) * piece16 + (f - i * piece16);
+  if (f < n16) dsp_st_stream(dsp_ld_stream(src + s), dst + f);
+}
+
+// The read of a decode batch with no arithmetic and no imbalance: workgroup w (KVH waves,
+// wave h reading KV head h) reads keys [k0, min(k0 + kKeys, ctx_b)) of sequence b, where
+// (b, k0) = work[w]; every key of every sequence once, the head slices of each slot row
+// side by side (as the balanced decode kernel reads them when its head group is the whole
+// row), K and V, addressed through the block table.  The host cuts every sequence into
+// kKeys-key pieces, so all workgroups but a sequence's last read the same bytes.
+constexpr int kSegKeys = 256;
+__global__ __launch_bounds__(512) void batch_read_kernel(const uint16_t* __restrict__ kc,
+                                                         const uint16_t* __restrict__ vc,
+                                                         int64_t num_slots,
+                                                         const int32_t* __restrict__ bt,
+                                                         int64_t bt_stride, int32_t log2_bs,
+                                                         const int32_t* __restrict__ ctx_lens,
+                                                         const int32_t* __restrict__ work,
+                                                         int32_t KVH, uint32_t* __restrict__ sink) {
+  constexpr int D = 128;
+  const int b = work[2 * blockIdx.x], k0 = work[2 * blockIdx.x + 1];
+  const int ctx = ctx_lens[b];
+  const int h = int(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int bmask = (1 << log2_bs) - 1;
+  const int k1 = min(k0 + kSegKeys, ctx);
+  dsp_u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int t = k0; t < k1; t += 32) {
+    dsp_u32x4 kv[8], vv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int key = min(t + i * 4 + lane / 16, k1 - 1);
+      int64_t slot = int64_t(bt[int64_t(b) * bt_stride + (key >> log2_bs)]) * (bmask + 1) +
+                     (key & bmask);
+      slot = (slot >= 0 && slot < num_slots) ? slot : 0;  // a bad block id reads row 0
+      const int64_t e = slot * (int64_t(KVH) * D) + int64_t(h) * D + (lane % 16) * 8;
+      kv[i] = *reinterpret_cast<const dsp_u32x4*>(kc + e);
+      vv[i] = *reinterpret_cast<const dsp_u32x4*>(vc + e);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc ^= kv[i] ^ vv[i];
+  }
+  const uint32_t r = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (r == 0x9e3779b9u) sink[0] = r;
+}
+
 // Stores only: piece i of dst (piece_bytes, a multiple of 4096) filled with a constant at
 // dst + dst_index[i] * piece_bytes -- the write half of the copies above, alone (the
 // copy-on-write fork's 32 copies of one block read it from L2 and write HBM only).  One
@@ -288,5 +344,36 @@ extern "C" int dsp_probe_piece_fill(void* dst, int64_t bytes, int64_t piece_byte
                       static_cast<hipStream_t>(stream)>>>(static_cast<dsp_u32x4*>(dst),
                                                           piece_bytes / 16, n16, dst_index,
                                                           0x3f803f80u);
+  return dsp_launch_status();
+}
+
+extern "C" int dsp_probe_piece_gather(const void* src, void* dst, int64_t bytes,
+                                      int64_t piece_bytes, const int32_t* src_index,
+                                      dsp_stream_t stream) {
+  DSP_HOST_CHECK(src && dst && src_index && bytes >= 16 && piece_bytes >= 4096, DSP_EINVAL);
+  DSP_HOST_CHECK(piece_bytes % 4096 == 0 && bytes % piece_bytes == 0, DSP_EINVAL);
+  DSP_HOST_CHECK(dsp_aligned(src, 16) && dsp_aligned(dst, 16), DSP_EALIGN);
+  const int64_t n16 = bytes / 16;
+  DSP_HOST_CHECK(n16 / 256 < (int64_t(1) << 31), DSP_EINVAL);
+  piece_gather_kernel<<<dim3(static_cast<unsigned>((n16 + 255) / 256)), 256, 0,
+                        static_cast<hipStream_t>(stream)>>>(
+      static_cast<const dsp_u32x4*>(src), static_cast<dsp_u32x4*>(dst), piece_bytes / 16, n16,
+      src_index);
+  return dsp_launch_status();
+}
+
+extern "C" int dsp_probe_batch_read(const void* k_cache, const void* v_cache, int64_t num_slots,
+                                    const int32_t* block_table, int64_t bt_stride,
+                                    int32_t block_size, const int32_t* ctx_lens,
+                                    const int32_t* work, int32_t num_work, int32_t KVH,
+                                    uint32_t* sink, dsp_stream_t stream) {
+  DSP_HOST_CHECK(k_cache && v_cache && block_table && ctx_lens && work && sink, DSP_EINVAL);
+  DSP_HOST_CHECK(num_work > 0 && KVH > 0 && KVH <= 8 && num_slots > 0, DSP_EINVAL);
+  DSP_HOST_CHECK(dsp_is_pow2(block_size), DSP_EINVAL);
+  DSP_HOST_CHECK(dsp_aligned(k_cache, 16) && dsp_aligned(v_cache, 16), DSP_EALIGN);
+  batch_read_kernel<<<dim3(static_cast<unsigned>(num_work)), 64 * KVH, 0,
+                      static_cast<hipStream_t>(stream)>>>(
+      static_cast<const uint16_t*>(k_cache), static_cast<const uint16_t*>(v_cache), num_slots,
+      block_table, bt_stride, dsp_log2i(block_size), ctx_lens, work, KVH, sink);
   return dsp_launch_status();
 }
