@@ -76,6 +76,11 @@ class HipGraphDecoder:
                  buckets: tuple[int, ...] = DEFAULT_BUCKETS):
         if not buckets or min(buckets) <= 0:
             raise ValueError(f"buckets must be positive context lengths, got {buckets}")
+        if runner.attn_backend != "hip":
+            # the native backend walks the host-side sequence list every step: a replay
+            # would attend with the lengths of the step that was captured
+            raise ValueError(f"HipGraphDecoder captures attn_backend='hip' (device-side batch "
+                             f"metadata); this runner uses {runner.attn_backend!r}")
         if cache.key.device.type != "cuda":
             raise RuntimeError("HipGraphDecoder needs the cache on a GPU")
         self.r = runner

@@ -55,3 +55,16 @@ def test_fused_projection_views_match_separate_projections():
                                    fused._mlp(fused.layers[i], x, i), rtol=1e-5, atol=1e-5)
     h = torch.randn(3, plain_model.config.hidden_size)
     torch.testing.assert_close(plain.logits(h, torch.tensor([2, 0])), plain.lm_head(h)[[2, 0]])
+
+
+def test_graph_decoder_needs_the_hip_backend():
+    """A HIP graph replays device-side batch metadata; the native backend reads the host
+    sequence list every step, so the graph decoder refuses it up front."""
+    from types import SimpleNamespace
+
+    from dispec_amd.engine.hip_graph import HipGraphDecoder
+    from dispec_amd.engine.model_runner import ModelRunner
+    runner = ModelRunner(toy_lm("qwen3"), attn_backend="native")
+    fake_cache = SimpleNamespace(key=torch.zeros(1))
+    with pytest.raises(ValueError, match="attn_backend='hip'"):
+        HipGraphDecoder(runner, fake_cache)
