@@ -417,14 +417,16 @@ def bench_c2(torch) -> dict:
 # ------------------------------------------------------------------ skewed decode batches
 def bench_skew(torch) -> dict:
     """Decode batches with uneven contexts (the serving case config 3's uniform batch does
-    not show), one layer, Qwen3-4B heads (Hq 32, KVH 8, D 128): 'skew' = one 32768-token
-    context beside 15 of 512; 'mixed' = 32 contexts ~U[16, 2048) with one of 16384.  Timed
-    with the automatic split (balanced: equal key shares per wave) and with fixed 1024-token
-    partitions, kernel-only, HIP events around each launch."""
+    not show), Qwen3-4B heads (Hq 32, KVH 8, D 128): 'skew' = one 32768-token context beside
+    15 of 512; 'mixed' = 32 contexts ~U[16, 2048) with one of 16384.  Timed with the
+    automatic split (balanced: equal key shares per wave) and with fixed 1024-token
+    partitions over a loop of 16 layers of their own K/V, as a model's step reads them (one
+    layer's 165-200 MB would otherwise stay in the 256 MB Infinity Cache between launches);
+    per-layer time = loop time / 16, HIP events around the loop."""
     from dispec_amd import _lib
     from dispec_amd.engine.hip_attn import paged_decode_attention_blocks
 
-    dev, Hq, KVH, D, bs = "cuda", 32, 8, 128, 16
+    dev, Hq, KVH, D, bs, L = "cuda", 32, 8, 128, 16, 16
     gcpu = torch.Generator().manual_seed(4001)
     mixed = torch.randint(16, 2048, (32,), generator=gcpu).tolist()
     mixed[3] = 16384
@@ -433,10 +435,10 @@ def bench_skew(torch) -> dict:
         B = len(ctxs)
         need = [-(-c // bs) for c in ctxs]
         NB = int(sum(need) * 1.25) + 8
-        kc = torch.empty((NB * bs, KVH, D), dtype=torch.bfloat16, device=dev)
+        kc = torch.empty((L, NB * bs, KVH, D), dtype=torch.bfloat16, device=dev)
         vc = torch.empty_like(kc)
-        _fill_randn(torch, kc.view(1, -1), 4002)
-        _fill_randn(torch, vc.view(1, -1), 4003)
+        _fill_randn(torch, kc, 4002)
+        _fill_randn(torch, vc, 4003)
         perm = torch.randperm(NB, generator=gcpu).tolist()
         bt = torch.zeros((B, max(need)), dtype=torch.int32)
         at = 0
@@ -455,19 +457,11 @@ def bench_skew(torch) -> dict:
         kv_bytes = sum(ctxs) * KVH * D * 2 * 2
         for label, P in (("balanced", 0), ("fixed1024", 1024)):
             def f():
-                paged_decode_attention_blocks(q, kc, vc, bt, ctx, Hq // KVH, block_size=bs,
-                                              max_ctx=max(ctxs), partition_tokens=P,
-                                              out=out, workspace=ws)
-            for _ in range(3):
-                f()
-            torch.cuda.synchronize()
-            ev = [_events(torch) for _ in range(20)]
-            for a, b in ev:
-                a.record()
-                f()
-                b.record()
-            torch.cuda.synchronize()
-            us = statistics.median(a.elapsed_time(b) for a, b in ev) * 1e3
+                for layer in range(L):
+                    paged_decode_attention_blocks(q, kc[layer], vc[layer], bt, ctx, Hq // KVH,
+                                                  block_size=bs, max_ctx=max(ctxs),
+                                                  partition_tokens=P, out=out, workspace=ws)
+            us = _time_gpu(torch, f, 5) / L * 1e6
             res[f"{name}_{label}_us"] = us
             res[f"{name}_{label}_GBps"] = kv_bytes / us / 1e3
         del kc, vc
@@ -479,19 +473,20 @@ def bench_skew(torch) -> dict:
 def _verify_skew(torch) -> dict:
     """A 5-query verify (Qwen3-1.7B heads: Hq 16, KVH 8, D 128) over one 32768-token context
     beside 15 of 512: the balanced split-K kernel (what ModelRunner picks for such a batch)
-    against the fixed key partitions the library sizes from max_ctx."""
+    against the fixed key partitions the library sizes from max_ctx; a loop over 16 layers
+    of their own K/V, as for the decode batches above."""
     from dispec_amd import _lib
     from dispec_amd.engine.hip_attn import paged_mq_attention
 
-    dev, Hq, KVH, D, bs, ql = "cuda", 16, 8, 128, 16, 5
+    dev, Hq, KVH, D, bs, ql, L = "cuda", 16, 8, 128, 16, 5, 16
     ctxs = [32768] + [512] * 15
     B = len(ctxs)
     need = [-(-c // bs) for c in ctxs]
     NB = int(sum(need) * 1.25) + 8
-    kc = torch.empty((NB * bs, KVH, D), dtype=torch.bfloat16, device=dev)
+    kc = torch.empty((L, NB * bs, KVH, D), dtype=torch.bfloat16, device=dev)
     vc = torch.empty_like(kc)
-    _fill_randn(torch, kc.view(1, -1), 4005)
-    _fill_randn(torch, vc.view(1, -1), 4006)
+    _fill_randn(torch, kc, 4005)
+    _fill_randn(torch, vc, 4006)
     perm = torch.randperm(NB, generator=torch.Generator().manual_seed(4007)).tolist()
     bt = torch.zeros((B, max(need)), dtype=torch.int32)
     at = 0
@@ -512,9 +507,11 @@ def _verify_skew(torch) -> dict:
     res = {}
     for label, bal in (("balanced", True), ("partitioned", False)):
         def f():
-            paged_mq_attention(q, kc, vc, bt, cu, ctx, Hq // KVH, block_size=bs, max_q_len=ql,
-                               max_ctx=max(ctxs), out=out, workspace=ws, balanced=bal)
-        us = _time_gpu(torch, f, 20) * 1e6
+            for layer in range(L):
+                paged_mq_attention(q, kc[layer], vc[layer], bt, cu, ctx, Hq // KVH,
+                                   block_size=bs, max_q_len=ql, max_ctx=max(ctxs), out=out,
+                                   workspace=ws, balanced=bal)
+        us = _time_gpu(torch, f, 5) / L * 1e6
         res[f"verify_skew_{label}_us"] = us
         res[f"verify_skew_{label}_GBps"] = kv_bytes / us / 1e3
     del kc, vc
