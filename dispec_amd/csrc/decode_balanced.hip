@@ -265,7 +265,12 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
       }
     };
     // V rows of chunk t0 into the slab: chunk c of row r at slot c ^ 2*((r >> 2) & 3).
-    // Rows past ke repeat row ke - 1 (finite data, probability exactly 0).
+    // Rows past ke repeat row ke - 1 (finite data, probability exactly 0).  Non-temporal
+    // (aux 2): a layer's V is read once per step and other layers evict it before the next,
+    // so keeping it in the caches only costs (same-box A/B over multi-layer loops: config 3
+    // 361.8-364.9 -> 351.0 us, config 2 41.0-41.3 -> 39.4-39.6, the skewed and mixed batches
+    // and the skewed verify 4-5 % faster; non-temporal K loads as well gained on config 2 but
+    // lost 2 % on config 3).
     auto load_v = [&](int t0) {
 #pragma unroll
       for (int i = 0; i < VINS; ++i) {
@@ -274,7 +279,7 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
         const uint16_t* src = addr(vc, (e >= 0 ? e : 0) + 8 * swz(row, sl));
         __builtin_amdgcn_global_load_lds(static_cast<const void*>(src),
                                          (__attribute__((address_space(3))) void*)(slab_l + i * 1024),
-                                         16, 0, 0);
+                                         16, 0, 2);
       }
     };
 
