@@ -431,9 +431,12 @@ __global__ __launch_bounds__(64 * HG) __attribute__((amdgpu_waves_per_eu(kOcc)))
 // sequence) a context outside [0, max_ctx]; for multi-query a context outside
 // [q_len, max_ctx], whose rows are written as zeros.  One pass with online
 // rescaling: wave w takes pieces w, w + 4, ..., each lane loading the (max, sum) pair and
-// its dims of the accumulator of 16 pieces at once, so the merge costs two dependent
-// memory round trips (ctx_lens, then the pieces) whatever the piece count; the waves'
-// partial merges meet in LDS.
+// its dims of the accumulator of up to 16 pieces at once, so the merge costs two dependent
+// memory round trips (ctx_lens, then the pieces) for up to 64 pieces; the waves' partial
+// merges meet in LDS.  The piece count is known (and wave-uniform) before the pieces are
+// loaded, so a wave issues loads for its own pieces only: loading all 16 through clamped
+// addresses and discarding the extra ones by a select cost ~1.3 us of L1 bandwidth per
+// launch on config 2 (9 pieces a segment).
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
@@ -444,18 +447,20 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
   constexpr int kInFlight = 16;       // pieces loaded per lane before they are folded in
   __shared__ float s_acc[4][NV * 64];
   __shared__ float s_ml[4][2];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int h = blockIdx.x, b = blockIdx.y, i = blockIdx.z;
   const int q0 = cu_q ? cu_q[b] : b;
   const int ql = cu_q ? cu_q[b + 1] - q0 : 1;
   if (i >= ql) return;
   const int maxq = RPH / G;  // max_q_len (the grid's z extent)
+  // total units, and the units of the sequences before b, from one scan per 64 sequences
   int64_t total = 0, pre = 0;
   for (int b0 = 0; b0 < B; b0 += 64) {
     const int bb = b0 + lane;
-    const int v = bb < B ? seq_units(ctx_lens, cu_q, bb, max_ctx, maxq) : 0;
-    total += wave_sum(v);
-    pre += wave_sum(bb < b ? v : 0);
+    const int incl = wave_incl_scan(bb < B ? seq_units(ctx_lens, cu_q, bb, max_ctx, maxq) : 0);
+    if (b >= b0 && b < b0 + 64)
+      pre = total + (b > b0 ? __builtin_amdgcn_readlane(incl, b - b0 - 1) : 0);
+    total += __builtin_amdgcn_readlane(incl, 63);
   }
   const int raw = ctx_lens[b];
   const bool bad = cu_q ? mq_bad(ql, raw, maxq, max_ctx) : (raw < 0 || raw > max_ctx);
@@ -484,17 +489,23 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
   float Mw = -INFINITY, Lw = 0.f, A[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) A[j] = 0.f;
-  for (int p = wave; p < np; p += 4 * kInFlight) {
+  const int npw = np > wave ? (np - wave + 3) >> 2 : 0;  // this wave's pieces: wave + 4k
+  for (int k0 = 0; k0 < npw; k0 += kInFlight) {
     float mv[kInFlight], lv[kInFlight], v[kInFlight][NV];
 #pragma unroll
     for (int u = 0; u < kInFlight; ++u) {
-      const int pp = p + 4 * u;
-      const bool in = pp < np;
-      const int64_t r = in ? int64_t(pp) * pstride : 0;
-      mv[u] = in ? ml[2 * r] : -INFINITY;
-      lv[u] = in ? ml[2 * r + 1] : 0.f;
+      if (k0 + u < npw) {  // wave-uniform: the loads of absent pieces are not issued
+        const int64_t r = int64_t(wave + 4 * (k0 + u)) * pstride;
+        mv[u] = ml[2 * r];
+        lv[u] = ml[2 * r + 1];
 #pragma unroll
-      for (int j = 0; j < NV; ++j) v[u][j] = in ? src[r * D + 64 * j] : 0.f;
+        for (int j = 0; j < NV; ++j) v[u][j] = src[r * D + 64 * j];
+      } else {
+        mv[u] = -INFINITY;
+        lv[u] = 0.f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) v[u][j] = 0.f;
+      }
     }
     float bm = Mw;
 #pragma unroll
