@@ -23,8 +23,9 @@ extern "C" {
  *     for each (sequence, KV head) `waves_per_seq_head` waves read that head's 128-dim
  *     bf16 row of K and V for all `ctx` keys through `block_table`, the waves of 4 heads
  *     of the same keys side by side in one workgroup when KVH % 4 == 0 (as the balanced
- *     decode kernel groups them); caches are [num_slots, KVH, 128] contiguous; ctx a
- *     multiple of 32 * waves_per_seq_head.
+ *     decode kernel groups them), K with cached loads and V non-temporal (as the decode
+ *     kernels load them); caches are [num_slots, KVH, 128] contiguous; ctx a multiple of
+ *     32 * waves_per_seq_head.
  * Both store one word to `sink` only if what they read hashes to a sentinel. */
 int dsp_probe_stream_read(const void* buf, int64_t bytes, int32_t workgroups, uint32_t* sink,
                           dsp_stream_t stream);
@@ -55,8 +56,8 @@ int dsp_probe_piece_gather(const void* src, void* dst, int64_t bytes, int64_t pi
                            const int32_t* src_index, dsp_stream_t stream);
 /*   dsp_probe_batch_read: the K/V read of a decode batch (head_dim 128, KVH <= 8) with no
  *     arithmetic and equal work per workgroup: workgroup w reads keys [k0, min(k0 + 256,
- *     ctx_lens[b])) of sequence b for all KV heads, (b, k0) = work[2w], work[2w + 1]; the
- *     floor of a decode's time on those contexts. */
+ *     ctx_lens[b])) of sequence b for all KV heads, (b, k0) = work[2w], work[2w + 1], K
+ *     cached and V non-temporal; the floor of a decode's time on those contexts. */
 int dsp_probe_batch_read(const void* k_cache, const void* v_cache, int64_t num_slots,
                          const int32_t* block_table, int64_t bt_stride, int32_t block_size,
                          const int32_t* ctx_lens, const int32_t* work, int32_t num_work,

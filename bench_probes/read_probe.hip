@@ -36,7 +36,8 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const dsp_u32x4* __res
 // One workgroup of HG waves per (sequence, group of HG KV heads, share of its keys), wave
 // i reading head HG*group + i, as the balanced decode kernel groups its waves: per 32 keys
 // a wave reads its head's row of K and of V for every key (16 bytes per lane, 4 rows per
-// load), addressed through the block table exactly as the decode kernels address the pool.
+// load), addressed through the block table exactly as the decode kernels address the pool,
+// with their cache policy: K cached, V non-temporal.
 template <int HG>
 __global__ __launch_bounds__(64 * HG) void slice_read_kernel(const uint16_t* __restrict__ kc,
                                                              const uint16_t* __restrict__ vc,
@@ -65,7 +66,7 @@ __global__ __launch_bounds__(64 * HG) void slice_read_kernel(const uint16_t* __r
       slot = (slot >= 0 && slot < num_slots) ? slot : 0;  // a bad block id reads row 0
       const int64_t e = slot * (int64_t(KVH) * D) + int64_t(h) * D + (lane % 16) * 8;
       kv[i] = *reinterpret_cast<const dsp_u32x4*>(kc + e);
-      vv[i] = *reinterpret_cast<const dsp_u32x4*>(vc + e);
+      vv[i] = dsp_ld_stream(reinterpret_cast<const dsp_u32x4*>(vc + e));
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc ^= kv[i] ^ vv[i];
@@ -139,8 +140,9 @@ __global__ __launch_bounds__(256) void piece_gather_kernel(const dsp_u32x4* __re
 // wave h reading KV head h) reads keys [k0, min(k0 + kKeys, ctx_b)) of sequence b, where
 // (b, k0) = work[w]; every key of every sequence once, the head slices of each slot row
 // side by side (as the balanced decode kernel reads them when its head group is the whole
-// row), K and V, addressed through the block table.  The host cuts every sequence into
-// kKeys-key pieces, so all workgroups but a sequence's last read the same bytes.
+// row), K and V (K cached, V non-temporal, as the decode kernel loads them), addressed
+// through the block table.  The host cuts every sequence into kKeys-key pieces, so all
+// workgroups but a sequence's last read the same bytes.
 constexpr int kSegKeys = 256;
 __global__ __launch_bounds__(512) void batch_read_kernel(const uint16_t* __restrict__ kc,
                                                          const uint16_t* __restrict__ vc,
@@ -167,7 +169,7 @@ __global__ __launch_bounds__(512) void batch_read_kernel(const uint16_t* __restr
       slot = (slot >= 0 && slot < num_slots) ? slot : 0;  // a bad block id reads row 0
       const int64_t e = slot * (int64_t(KVH) * D) + int64_t(h) * D + (lane % 16) * 8;
       kv[i] = *reinterpret_cast<const dsp_u32x4*>(kc + e);
-      vv[i] = *reinterpret_cast<const dsp_u32x4*>(vc + e);
+      vv[i] = dsp_ld_stream(reinterpret_cast<const dsp_u32x4*>(vc + e));
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc ^= kv[i] ^ vv[i];
