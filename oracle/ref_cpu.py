@@ -8,7 +8,10 @@ Each function restates one step of the reference algorithm and cites the referen
 file:line it follows.  bf16 data is carried as uint16 bit patterns (numpy has no bf16);
 `bf16_to_f32` widens exactly and `f32_to_bf16` rounds to nearest even, as torch does.
 
-How each function is pinned (tests/test_oracle_*.py):
+How each function is pinned (tests/test_oracle*.py; tests/test_oracle_mutants.py runs
+edited copies of this module's source -- wrong KV head, dropped scale, swapped operand,
+wrong softmax axis, short causal mask, wrong block index -- through the same kinds of
+checks and requires each to fail one):
   slot math ............ known answers of tests/test_block_manager.py:8-27 and a
                          brute-force walk of the block table
   append/gather/export/

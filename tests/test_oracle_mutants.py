@@ -1,0 +1,115 @@
+"""The oracle's pins catch plausible slips (CPU only).
+
+Each mutant below is the oracle module itself with one edit applied to its source text
+-- the kind of slip a restatement can make: a query head served by the wrong KV head, a
+dropped softmax scale, scores taken against V instead of K, a softmax normalised over
+the wrong axis, a causal mask one key short, a slot computed from the wrong block index.
+The edited module is executed in a fresh namespace and run through the same kinds of
+checks tests/test_oracle.py pins the real oracle with: torch's SDPA (with enable_gqa and
+causal_lower_right, the routines the reference path calls) and the reference's known slot
+answers (tests/test_block_manager.py:8-15).  Every mutant must fail at least one check,
+and the unedited source must pass all of them, so the checks are shown to tell a right
+restatement from a wrong one.
+"""
+
+import inspect
+import types
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from torch.nn.attention.bias import causal_lower_right
+
+from oracle import ref_cpu
+from tests._util import gen
+
+_SOURCE = inspect.getsource(ref_cpu)
+
+# (name, text in the oracle's source, replacement, occurrences to edit)
+MUTANTS = [
+    ("kv head h % KVH instead of h // G",
+     "np.repeat(np.asarray(k_cache[slots], dtype=np.float64), kv_groups, axis=1)",
+     "np.tile(np.asarray(k_cache[slots], dtype=np.float64), (1, kv_groups, 1))", 2),
+    ("decode scale dropped", "[:, :, 0] * scale  # (Hq, n)", "[:, :, 0]  # (Hq, n)", 1),
+    ("decode scores against V", "np.matmul(k.transpose(1, 0, 2), q[b][:, :, None])",
+     "np.matmul(v.transpose(1, 0, 2), q[b][:, :, None])", 1),
+    ("decode softmax over the heads", "p /= p.sum(axis=1, keepdims=True)",
+     "p /= p.sum(axis=0, keepdims=True)", 1),
+    ("causal mask one key short", "<= np.arange(q_len)[:, None] + past",
+     "< np.arange(q_len)[:, None] + past", 1),
+    ("multi-query scale dropped", "k.transpose(1, 2, 0)) * scale",
+     "k.transpose(1, 2, 0))", 1),
+    ("slot from the position, not its block", "return bt[p // block_size] * block_size + p % block_size",
+     "return bt[p % len(bt)] * block_size + p % block_size", 1),
+]
+
+
+def _module(source: str) -> types.ModuleType:
+    mod = types.ModuleType("ref_cpu_variant")
+    exec(compile(source, "ref_cpu_variant", "exec"), mod.__dict__)
+    return mod
+
+
+def _decode_agrees(m) -> bool:
+    Hq, KVH, D, S = 14, 2, 32, 256
+    q = torch.randn((3, Hq, D), generator=gen(70), dtype=torch.float64)
+    kc = torch.randn((S, KVH, D), generator=gen(71), dtype=torch.float64)
+    vc = torch.randn((S, KVH, D), generator=gen(72), dtype=torch.float64)
+    lens = [1, 90, 41]
+    st = torch.zeros((3, 90), dtype=torch.long)
+    for i, n in enumerate(lens):
+        st[i, :n] = torch.randperm(S, generator=gen(73 + i))[:n]
+    ours = m.decode_attention(q.numpy(), kc.numpy(), vc.numpy(), st.numpy(), lens, Hq // KVH)
+    for b, n in enumerate(lens):
+        s = st[b, :n]
+        lib = F.scaled_dot_product_attention(q[b][None, :, None], kc[s].transpose(0, 1)[None],
+                                             vc[s].transpose(0, 1)[None], enable_gqa=True)
+        if not np.allclose(ours[b], lib[0, :, 0].numpy(), atol=1e-10):
+            return False
+    return True
+
+
+def _mq_agrees(m) -> bool:
+    for q_len, ctx in ((5, 19), (3, 3), (1, 12)):
+        g = gen(80 + q_len * 31 + ctx)
+        q = torch.randn(1, 4, q_len, 16, generator=g, dtype=torch.float64)
+        k = torch.randn(1, 2, ctx, 16, generator=g, dtype=torch.float64)
+        v = torch.randn(1, 2, ctx, 16, generator=g, dtype=torch.float64)
+        lib = F.scaled_dot_product_attention(q, k, v, attn_mask=causal_lower_right(q_len, ctx),
+                                             enable_gqa=True)
+        ours = m.mq_attention(q[0].permute(1, 0, 2).numpy(), k[0].permute(1, 0, 2).numpy(),
+                              v[0].permute(1, 0, 2).numpy(), [np.arange(ctx)], [q_len], 2)
+        if not np.allclose(ours, lib[0].permute(1, 0, 2).numpy(), atol=1e-10):
+            return False
+    return True
+
+
+def _slots_agree(m) -> bool:
+    # tests/test_block_manager.py:8-15: bs=4, token 0 -> (block 0, 0), token 5 -> (block 1, 1)
+    ids = [7, 3, 9]
+    return (int(m.slots_for_positions(ids, [0], 4)[0]) == 7 * 4 + 0 and
+            int(m.slots_for_positions(ids, [5], 4)[0]) == 3 * 4 + 1 and
+            int(m.slots_for_positions(ids, [10], 4)[0]) == 9 * 4 + 2)
+
+
+def _passes_all(m) -> bool:
+    checks = (_decode_agrees, _mq_agrees, _slots_agree)
+    for check in checks:
+        try:
+            if not check(m):
+                return False
+        except (ValueError, IndexError):  # a mutant may also fail loudly
+            return False
+    return True
+
+
+def test_unedited_oracle_passes_every_check():
+    assert _passes_all(_module(_SOURCE))
+
+
+@pytest.mark.parametrize("name,old,new,count", MUTANTS, ids=[m[0] for m in MUTANTS])
+def test_each_slip_fails_a_check(name, old, new, count):
+    assert _SOURCE.count(old) == count, f"the oracle's source no longer holds {old!r}"
+    mutant = _module(_SOURCE.replace(old, new))
+    assert not _passes_all(mutant), f"no check tells the oracle from its mutant: {name}"
