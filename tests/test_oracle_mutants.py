@@ -3,12 +3,15 @@
 Each mutant below is the oracle module itself with one edit applied to its source text
 -- the kind of slip a restatement can make: a query head served by the wrong KV head, a
 dropped softmax scale, scores taken against V instead of K, a softmax normalised over
-the wrong axis, a causal mask one key short, a slot computed from the wrong block index.
+the wrong axis, a causal mask one key short, a slot computed from the wrong block index,
+an append that writes its rows in the wrong order, a block copy run backwards, an export
+that walks the block table backwards.
 The edited module is executed in a fresh namespace and run through the same kinds of
 checks tests/test_oracle.py pins the real oracle with: torch's SDPA (with enable_gqa and
-causal_lower_right, the routines the reference path calls) and the reference's known slot
-answers (tests/test_block_manager.py:8-15).  Every mutant must fail at least one check,
-and the unedited source must pass all of them, so the checks are shown to tell a right
+causal_lower_right), `index_copy_` and advanced indexing (the routines the reference path
+calls), the reference's known slot answers (tests/test_block_manager.py:8-15) and a
+hand-built block-copy answer.  Every mutant must fail at least one check, and the
+unedited source must pass all of them, so the checks are shown to tell a right
 restatement from a wrong one.
 """
 
@@ -21,7 +24,7 @@ import torch
 import torch.nn.functional as F
 from torch.nn.attention.bias import causal_lower_right
 
-from oracle import ref_cpu
+from oracle import ref_cpu, ref_torch
 from tests._util import gen
 
 _SOURCE = inspect.getsource(ref_cpu)
@@ -42,6 +45,13 @@ MUTANTS = [
      "k.transpose(1, 2, 0))", 1),
     ("slot from the position, not its block", "return bt[p // block_size] * block_size + p % block_size",
      "return bt[p % len(bt)] * block_size + p % block_size", 1),
+    ("append rows in reverse order", "    pool_layer[slots] = rows\n",
+     "    pool_layer[slots] = rows[::-1]\n", 1),
+    ("block copy run backwards", "src_pool[:, s * block_size:(s + 1) * block_size]",
+     "src_pool[:, d * block_size:(d + 1) * block_size]", 1),
+    ("export walks the table backwards",
+     "np.ascontiguousarray(pool[:, context_slots(block_ids, seq_len, block_size)])",
+     "np.ascontiguousarray(pool[:, context_slots(block_ids[::-1], seq_len, block_size)])", 1),
 ]
 
 
@@ -93,8 +103,34 @@ def _slots_agree(m) -> bool:
             int(m.slots_for_positions(ids, [10], 4)[0]) == 9 * 4 + 2)
 
 
+def _u16(t):
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _byte_moves_agree(m) -> bool:
+    key = torch.randn((3, 96, 2, 4), generator=gen(90)).to(torch.bfloat16)
+    slots = torch.randperm(96, generator=gen(91))[:13]
+    rows = torch.randn((13, 2, 4), generator=gen(92)).to(torch.bfloat16)
+    ours = _u16(key).copy()
+    m.append(ours[1], slots.numpy(), _u16(rows))
+    theirs = key.clone()
+    theirs[1].index_copy_(0, slots, rows)
+    if not np.array_equal(ours, _u16(theirs)):
+        return False
+    ids, n = [5, 0, 2], 37
+    tslots = ref_torch.context_slots(ids, n, 16)
+    if not np.array_equal(m.export_contiguous(_u16(key), ids, n, 16), _u16(key[:, tslots])):
+        return False
+    # hand-built known answer: L = 2, 6 blocks of 2 slots, rows numbered in order
+    pool = np.arange(2 * 6 * 2, dtype=np.uint16).reshape(2, 6 * 2, 1, 1)
+    m.copy_blocks(pool, pool, [(0, 5), (3, 1)], 2)
+    return (pool[0, 10:12].ravel().tolist() == [0, 1] and
+            pool[1, 10:12].ravel().tolist() == [12, 13] and
+            pool[0, 2:4].ravel().tolist() == [6, 7] and pool[0, 0:2].ravel().tolist() == [0, 1])
+
+
 def _passes_all(m) -> bool:
-    checks = (_decode_agrees, _mq_agrees, _slots_agree)
+    checks = (_decode_agrees, _mq_agrees, _slots_agree, _byte_moves_agree)
     for check in checks:
         try:
             if not check(m):
