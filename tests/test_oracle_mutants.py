@@ -5,12 +5,14 @@ Each mutant below is the oracle module itself with one edit applied to its sourc
 dropped softmax scale, scores taken against V instead of K, a softmax normalised over
 the wrong axis, a causal mask one key short, a slot computed from the wrong block index,
 an append that writes its rows in the wrong order, a block copy run backwards, an export
-that walks the block table backwards.
+that walks the block table backwards, a RoPE frequency or rotation sign wrong, a map's
+design row in the wrong feature order, its bias or its residual's GELU dropped.
 The edited module is executed in a fresh namespace and run through the same kinds of
 checks tests/test_oracle.py pins the real oracle with: torch's SDPA (with enable_gqa and
 causal_lower_right), `index_copy_` and advanced indexing (the routines the reference path
-calls), the reference's known slot answers (tests/test_block_manager.py:8-15) and a
-hand-built block-copy answer.  Every mutant must fail at least one check, and the
+calls), transformers' Qwen3 rotary module, the reference's known answers (slot math,
+tests/test_block_manager.py:8-15; the map's feature order, tests/test_kv_transfer.py:89-100)
+and hand-built ones (a block copy, a quarter-turn rotation).  Every mutant must fail at least one check, and the
 unedited source must pass all of them, so the checks are shown to tell a right
 restatement from a wrong one.
 """
@@ -52,6 +54,15 @@ MUTANTS = [
     ("export walks the table backwards",
      "np.ascontiguousarray(pool[:, context_slots(block_ids, seq_len, block_size)])",
      "np.ascontiguousarray(pool[:, context_slots(block_ids[::-1], seq_len, block_size)])", 1),
+    ("rope frequency exponent halved", ".astype(np.float32) / head_dim))",
+     ".astype(np.float32) / (2 * head_dim)))", 1),
+    ("rotate-half sign flipped", "np.concatenate([-x[..., h:], x[..., :h]], axis=-1)",
+     "np.concatenate([x[..., h:], -x[..., :h]], axis=-1)", 1),
+    ("design row dims before heads", "np.ascontiguousarray(sel.transpose(1, 0, 2, 3))",
+     "np.ascontiguousarray(sel.transpose(1, 0, 3, 2))", 1),
+    ("map bias dropped", "    y = y + np.asarray(bias, np.float64)\n", "    y = y\n", 1),
+    ("residual GELU dropped", "y = y + _gelu(x @ down_w.T + down_b) @ up_w.T",
+     "y = y + (x @ down_w.T + down_b) @ up_w.T", 1),
 ]
 
 
@@ -129,8 +140,45 @@ def _byte_moves_agree(m) -> bool:
             pool[0, 2:4].ravel().tolist() == [6, 7] and pool[0, 0:2].ravel().tolist() == [0, 1])
 
 
+def _rope_agrees(m) -> bool:
+    from transformers import Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RotaryEmbedding
+    cfg = Qwen3Config(hidden_size=64, num_attention_heads=4, num_key_value_heads=2,
+                      head_dim=16, rope_theta=1e6, num_hidden_layers=1, vocab_size=16)
+    pos = torch.arange(200)
+    cos, sin = Qwen3RotaryEmbedding(cfg)(torch.zeros(1, 1), pos[None])
+    ours_c, ours_s = m.rope_tables(pos.numpy(), 16, 1e6)
+    if not (np.allclose(ours_c, cos[0].numpy(), atol=2e-6) and
+            np.allclose(ours_s, sin[0].numpy(), atol=2e-6)):
+        return False
+    # a quarter turn maps the halves (x1, x2) to (-x2, x1)
+    y = m.apply_rope(np.array([[[[1, 2, 3, 4]]]], np.float32), np.zeros((1, 4), np.float32),
+                     np.ones((1, 4), np.float32))
+    return y.ravel().tolist() == [-3, -4, 1, 2]
+
+
+def _map_agrees(m) -> bool:
+    g = np.random.default_rng(12)
+    src = g.standard_normal((3, 5, 2, 4))
+    x = m.design_rows(src, (2, 0))
+    # tests/test_kv_transfer.py:89-100: a row is the source layers in map order, each
+    # layer's heads then dims
+    if not all(np.array_equal(x[t], np.concatenate([src[2, t].ravel(), src[0, t].ravel()]))
+               for t in range(5)):
+        return False
+    W, b = g.standard_normal((16, 8)), g.standard_normal(8)
+    down_w, down_b, up_w = g.standard_normal((3, 16)), g.standard_normal(3), g.standard_normal((8, 3))
+    got = m.layer_map_apply(x, W, b, residual=(down_w, down_b, up_w))
+    xt = torch.from_numpy(x)
+    expect = F.linear(xt, torch.from_numpy(W).T, torch.from_numpy(b)) + F.linear(
+        F.gelu(F.linear(xt, torch.from_numpy(down_w), torch.from_numpy(down_b))),
+        torch.from_numpy(up_w))
+    return np.allclose(got, expect.numpy())
+
+
 def _passes_all(m) -> bool:
-    checks = (_decode_agrees, _mq_agrees, _slots_agree, _byte_moves_agree)
+    checks = (_decode_agrees, _mq_agrees, _slots_agree, _byte_moves_agree, _rope_agrees,
+              _map_agrees)
     for check in checks:
         try:
             if not check(m):
