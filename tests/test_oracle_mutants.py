@@ -6,11 +6,12 @@ dropped softmax scale, scores taken against V instead of K, a softmax normalised
 the wrong axis, a causal mask one key short, a slot computed from the wrong block index,
 an append that writes its rows in the wrong order, a block copy run backwards, an export
 that walks the block table backwards, a RoPE frequency or rotation sign wrong, a map's
-design row in the wrong feature order, its bias or its residual's GELU dropped.
+design row in the wrong feature order, its bias or its residual's GELU dropped, the
+attention prologue's norm weight left out or k normalised with q's weight.
 The edited module is executed in a fresh namespace and run through the same kinds of
 checks tests/test_oracle.py pins the real oracle with: torch's SDPA (with enable_gqa and
 causal_lower_right), `index_copy_` and advanced indexing (the routines the reference path
-calls), transformers' Qwen3 rotary module, the reference's known answers (slot math,
+calls), transformers' Qwen3 rotary and RMSNorm modules, the reference's known answers (slot math,
 tests/test_block_manager.py:8-15; the map's feature order, tests/test_kv_transfer.py:89-100)
 and hand-built ones (a block copy, a quarter-turn rotation).  Every mutant must fail at least one check, and the
 unedited source must pass all of them, so the checks are shown to tell a right
@@ -63,6 +64,11 @@ MUTANTS = [
     ("map bias dropped", "    y = y + np.asarray(bias, np.float64)\n", "    y = y\n", 1),
     ("residual GELU dropped", "y = y + _gelu(x @ down_w.T + down_b) @ up_w.T",
      "y = y + (x @ down_w.T + down_b) @ up_w.T", 1),
+    ("norm weight left out",
+     "return round_bf16(bf16_to_f32(w_bits) * round_bf16((x * inv).astype(np.float32)))",
+     "return round_bf16(round_bf16((x * inv).astype(np.float32)))", 1),
+    ("k normalised with q's weight", "rms_norm_bf16(k_bits, kw_bits, eps)",
+     "rms_norm_bf16(k_bits, qw_bits, eps)", 1),
 ]
 
 
@@ -176,9 +182,48 @@ def _map_agrees(m) -> bool:
     return np.allclose(got, expect.numpy())
 
 
+def _prologue_agrees(m) -> bool:
+    """transformers' Qwen3RMSNorm, the rotate-half RoPE and index_copy_ as torch bf16 ops
+    (model_runner.py:142-148), elementwise within one bf16 ulp, >= 99.9 % identical."""
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+    g = gen(60)
+    T, Hq, KVH, D = 5, 4, 2, 64
+    q = torch.randn((T, Hq, D), generator=g).to(torch.bfloat16)
+    k = torch.randn((T, KVH, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((T, KVH, D), generator=g).to(torch.bfloat16)
+    wq = (1 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    wk = (1 + 0.3 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    cos_f, sin_f = ref_cpu.rope_tables(np.arange(100, 100 + T), D, 1e6)
+    cos, sin = torch.from_numpy(cos_f).to(torch.bfloat16), torch.from_numpy(sin_f).to(torch.bfloat16)
+    qn, kn = Qwen3RMSNorm(D, eps=1e-6).to(torch.bfloat16), Qwen3RMSNorm(D, eps=1e-6).to(torch.bfloat16)
+    qn.weight.data.copy_(wq)
+    kn.weight.data.copy_(wk)
+
+    def rope(x):
+        x1, x2 = x.chunk(2, dim=-1)
+        return x * cos.unsqueeze(1) + torch.cat((-x2, x1), dim=-1) * sin.unsqueeze(1)
+
+    slots = torch.tensor([7, 0, 12, 3, 9])
+    kpool = torch.randn((16, KVH, D), generator=gen(61)).to(torch.bfloat16)
+    vpool = torch.randn((16, KVH, D), generator=gen(62)).to(torch.bfloat16)
+    with torch.no_grad():
+        tq, tk = rope(qn(q)), rope(kn(k))
+        tkp = kpool.clone()
+        tkp.index_copy_(0, slots, tk)
+    ok, ov = _u16(kpool), _u16(vpool)
+    oq = m.qk_norm_rope_append(_u16(q), _u16(k), _u16(v), _u16(wq), _u16(wk), 1e-6, _u16(cos),
+                               _u16(sin), slots.numpy(), ok, ov)
+    for got, want in ((oq, _u16(tq)), (ok, _u16(tkp))):
+        err = np.abs(ref_cpu.bf16_to_f32(got) - ref_cpu.bf16_to_f32(want))
+        ulp = np.abs(ref_cpu.bf16_to_f32(want)) * 2.0 ** -7 + 1e-30
+        if float((got == want).mean()) < 0.999 or not (err <= ulp).all():
+            return False
+    return True
+
+
 def _passes_all(m) -> bool:
     checks = (_decode_agrees, _mq_agrees, _slots_agree, _byte_moves_agree, _rope_agrees,
-              _map_agrees)
+              _map_agrees, _prologue_agrees)
     for check in checks:
         try:
             if not check(m):
