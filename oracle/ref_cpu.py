@@ -12,7 +12,7 @@ How each function is pinned (tests/test_oracle*.py; tests/test_oracle_mutants.py
 edited copies of this module's source -- wrong KV head, dropped scale, swapped operand,
 wrong softmax axis, short causal mask, wrong block index, reversed append or copy, wrong
 RoPE frequency or sign, wrong feature order, dropped bias, GELU or norm weight, k
-normalised with q's weight -- through the same
+normalised with q's weight, a bf16 map rounding or RoPE step missed -- through the same
 kinds of checks and requires each to fail one):
   slot math ............ known answers of tests/test_block_manager.py:8-27 and a
                          brute-force walk of the block table

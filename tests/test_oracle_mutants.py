@@ -7,7 +7,9 @@ the wrong axis, a causal mask one key short, a slot computed from the wrong bloc
 an append that writes its rows in the wrong order, a block copy run backwards, an export
 that walks the block table backwards, a RoPE frequency or rotation sign wrong, a map's
 design row in the wrong feature order, its bias or its residual's GELU dropped, the
-attention prologue's norm weight left out or k normalised with q's weight.
+attention prologue's norm weight left out or k normalised with q's weight, the bf16 map's
+GEMM result not rounded before its bias, its keys mapped without stripping RoPE, its
+values rotated.
 The edited module is executed in a fresh namespace and run through the same kinds of
 checks tests/test_oracle.py pins the real oracle with: torch's SDPA (with enable_gqa and
 causal_lower_right), `index_copy_` and advanced indexing (the routines the reference path
@@ -69,6 +71,13 @@ MUTANTS = [
      "return round_bf16(round_bf16((x * inv).astype(np.float32)))", 1),
     ("k normalised with q's weight", "rms_norm_bf16(k_bits, kw_bits, eps)",
      "rms_norm_bf16(k_bits, qw_bits, eps)", 1),
+    ("map GEMM not rounded before the bias",
+     'y = round_bf16((x @ np.asarray(m["weight"], np.float64)).astype(np.float32))',
+     'y = (x @ np.asarray(m["weight"], np.float64)).astype(np.float32)', 1),
+    ("keys mapped without stripping RoPE",
+     "content = f32_to_bf16(strip_rope(bf16_to_f32(k_bits), *source_rope))",
+     "content = np.asarray(k_bits, dtype=np.uint16)", 1),
+    ("values rotated too", "run(vals, value_maps, None)", "run(vals, value_maps, target_rope)", 1),
 ]
 
 
@@ -221,9 +230,39 @@ def _prologue_agrees(m) -> bool:
     return True
 
 
+def _bf16_map_agrees(m) -> bool:
+    g = gen(64)
+    L, T, H, D = 3, 11, 2, 8
+    k = torch.randn((L, T, H, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((L, T, H, D), generator=g).to(torch.bfloat16)
+    # identity maps between models with the same RoPE: values come back bit for bit, keys
+    # within the two roundings of strip -> bf16 -> apply (each element mixes with its
+    # partner half a head away, so the bound scales with the larger of the two)
+    cos, sin = ref_cpu.rope_tables(np.arange(40, 40 + T), D, 1e4)
+    eye = {"weight": np.eye(H * D), "bias": np.zeros(H * D)}
+    maps = [dict(eye, source_layers=(i,)) for i in range(L)]
+    km, vm = m.cross_model_map_bf16(_u16(k), _u16(v), maps, maps, (cos, sin), (cos, sin))
+    if not np.array_equal(vm, _u16(v)):
+        return False
+    kf = k.float().numpy()
+    mag = np.maximum(np.abs(kf), np.abs(np.roll(kf, D // 2, axis=-1)))
+    if not (np.abs(ref_cpu.bf16_to_f32(km) - kf) <= mag * 2.0 ** -6 + 1e-6).all():
+        return False
+    # a random bf16 map: exact GEMM rounded to bf16, then the bias added in bf16
+    # (transfer.py:104-112 as torch bf16 ops)
+    W = torch.randn((2 * H * D, H * D), generator=g).to(torch.bfloat16)
+    b = torch.randn((H * D,), generator=g).to(torch.bfloat16)
+    mm = [{"source_layers": (2, 0), "weight": W.float().numpy(), "bias": b.float().numpy()}]
+    ones, zeros = np.ones((T, D), np.float32), np.zeros((T, D), np.float32)
+    _, vm = m.cross_model_map_bf16(_u16(k), _u16(v), mm, mm, (ones, zeros), (ones, zeros))
+    x = v[[2, 0]].permute(1, 0, 2, 3).reshape(T, -1)
+    y = (x.double() @ W.double()).float().to(torch.bfloat16) + b
+    return np.array_equal(vm[0], _u16(y.view(T, H, D)))
+
+
 def _passes_all(m) -> bool:
     checks = (_decode_agrees, _mq_agrees, _slots_agree, _byte_moves_agree, _rope_agrees,
-              _map_agrees, _prologue_agrees)
+              _map_agrees, _prologue_agrees, _bf16_map_agrees)
     for check in checks:
         try:
             if not check(m):
