@@ -648,6 +648,9 @@ bool balanced_decode_applies(int32_t B, int32_t KVH, int32_t D, int32_t max_ctx,
   if (B < 1 || B > kMaxBatch || KVH < 1 || max_ctx < 1) return false;
   if (block_size < (1 << kLog2Unit)) return false;
   if (D != 32 && D != 64 && D != 128) return false;
+  // the unit scans (here and in the merge) add up 64 sequences' unit counts in 32-bit
+  // lanes: at most 64 x (2^25 - 1) units, i.e. contexts below 2^29 - 15 tokens
+  if (max_ctx > (1 << 29) - 16) return false;
   // w * C stays far inside int64 for every worker index w
   const int64_t cmax = int64_t(B) * KVH * ((int64_t(max_ctx) + 15) >> kLog2Unit);
   return cmax < (int64_t(1) << 40);

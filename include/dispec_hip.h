@@ -21,8 +21,8 @@
  *     calls stay independent) and (b) the 32 MiB scratch array of
  *     dsp_paged_decode_noalloc, shared by every call of that one entry point on a
  *     device (overlapping calls of it race; every other entry point is reentrant
- *     across streams).  Host-side, the library keeps only that array's per-device
- *     address once looked up.
+ *     across streams).  Host-side, the library caches two per-device values read once
+ *     from the runtime: that array's address and the device's compute-unit count.
  *   - Return value: 0 on success, a negative DSP_E* code for an invalid argument
  *     (nothing was launched), or a positive hipError_t from the launch.
  *   - `err_count` (optional, may be NULL) is a device int32 that the kernels

@@ -117,6 +117,13 @@ def test_partition_and_workspace_sizing(lib):
     # the balanced split asked for explicitly: its workspace alone
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, _lib.DSP_SPLIT_BALANCED) == \
         (4 * 2 + 64) * 7 * 66 * 4
+    # its unit scans add 64 sequences' 16-key unit counts in 32-bit lanes: contexts up to
+    # 2^29 - 16 tokens, none beyond (the automatic split then takes fixed partitions)
+    bal = _lib.DSP_SPLIT_BALANCED
+    assert lib.dsp_paged_decode_workspace_bytes(1, 2, 1, 64, (1 << 29) - 16, bal) > 0
+    assert lib.dsp_paged_decode_workspace_bytes(1, 2, 1, 64, (1 << 29) - 15, bal) == 0
+    assert lib.dsp_paged_mq_workspace_bytes(1, 2, 1, 64, 5, (1 << 29) - 15, bal) == 0
+    assert lib.dsp_paged_decode_workspace_bytes(1, 2, 1, 64, (1 << 29) - 15, 0) > 0
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 2, 64, 500, -2) == 0
     assert lib.dsp_paged_decode_workspace_bytes(4, 14, 3, 64, 500, 0) == 0     # 14 % 3 != 0
     # head_dim 256 (generic kernel): 1024-token partitions halved while the launch has fewer
