@@ -45,6 +45,47 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(_lib.SIGNATURES) == names, "ctypes prototypes out of sync with the header"
 
 
+def _header_prototypes() -> dict[str, tuple[str, list[str]]]:
+    """name -> (return type, parameter types) of every dsp_* declaration, types with the
+    parameter names dropped and whitespace normalised ('const int32_t*', 'float', ...)."""
+    text = (ROOT / "include" / "dispec_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for ret, name, params in re.findall(
+            r"^\s*((?:const\s+)?\w+\s*\*?)\s*(dsp_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+        types = []
+        for p in params.split(","):
+            p = " ".join(p.replace("*", "* ").split())
+            if p != "void":
+                types.append(re.sub(r"\s+\w+$", "", p).replace(" *", "*"))
+        out[name] = (ret.replace(" ", ""), types)
+    return out
+
+
+def test_ctypes_prototypes_match_header_types():
+    """Every argument's ctypes type has the width and kind of the header's C type: a
+    pointer for a pointer, c_int64 for int64_t, c_int32 for int32_t / int, c_size_t for
+    size_t, c_float for float.  ctypes passes whatever it is told, so an int32 / int64 swap
+    here would reach the kernels as a wrong value with no error."""
+    from dispec_amd import _lib
+    scalar = {"int64_t": ctypes.c_int64, "int32_t": ctypes.c_int32, "int": ctypes.c_int32,
+              "size_t": ctypes.c_size_t, "float": ctypes.c_float}
+    protos = _header_prototypes()
+    assert set(protos) == set(_lib.SIGNATURES)
+    for name, (ret, params) in protos.items():
+        restype, argtypes = _lib.SIGNATURES[name]
+        want_ret = ctypes.c_char_p if ret == "constchar*" else scalar[ret]
+        assert restype is want_ret, (name, ret, restype)
+        assert len(argtypes) == len(params), (name, len(argtypes), len(params))
+        for i, (c_type, ct) in enumerate(zip(params, argtypes)):
+            if c_type.endswith("*") or c_type == "dsp_stream_t":   # dsp_stream_t: void*
+                ok = ct is ctypes.c_void_p or (
+                    c_type.replace("const ", "") == "int64_t*" and ct is _lib._I64P)
+            else:
+                ok = ct is scalar[c_type]
+            assert ok, f"{name} argument {i}: header {c_type!r}, ctypes {ct.__name__}"
+
+
 def test_status_strings_and_version(lib):
     from dispec_amd import _lib
     assert lib.dsp_version() >= 1
