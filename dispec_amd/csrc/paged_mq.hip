@@ -312,9 +312,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3))) v
   }
 }
 
-// Merge the key partitions of one (tile, KV head, sequence).  Grid = (tiles * 16 / R, KVH,
-// B), R = mq_combine_rows(D) rows per workgroup: one thread per (row, 4 dims) output, its
-// accumulator elements one 16-byte load per partition.  Every thread folds its row's
+// Merge the key partitions of one (tile, KV head, sequence).  Grid = (ceil(rows_max / R),
+// KVH, B), R = mq_combine_rows(D) rows per workgroup (workgroup x takes packed rows x*R ..
+// x*R + R - 1 of the sequence's 16-row tiles): one thread per (row, 4 dims) output, its
+// accumulator elements one 16-byte load per partition.  rows_max = max_q_len * G bounds the
+// rows any valid sequence has, so threads of rows at or past it load nothing: a tile's
+// rows past it (6 of 16 for 5 queries of 2 heads, 14 for one query)
+// would otherwise fetch partitions that no valid row reads (FETCH_SIZE per merge, config
+// 4: verify 10.9 -> 7.0 MB, fork decode 21.7 -> 3.0 MB; fork decode step 21.0 -> 19.8 us
+// per layer on one box, verify unchanged).  Every thread folds its row's
 // partitions itself, 16 at a time with a running maximum, so the merge waits on one memory
 // round trip: the first 16 partitions' (max, sum) pairs and its accumulator elements are
 // loaded together with the sequence's lengths, before it is known how many of them the
@@ -327,7 +333,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ cu_q, const int32_t* __restrict__ ctx_lens, int32_t max_ctx,
     int32_t G, int32_t P, int32_t num_parts, int32_t tiles_max, int32_t prefix_tokens,
-    uint16_t* __restrict__ out, int64_t ost, int64_t osh) {
+    int32_t rows_max, uint16_t* __restrict__ out, int64_t ost, int64_t osh) {
   constexpr int TPR = D / 4;                // threads per row
   constexpr int R = mq_combine_rows(D);     // rows per workgroup
   constexpr int kBatch = 16;                // partitions in flight per thread
@@ -336,6 +342,10 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
   const int kvh = blockIdx.y, b = blockIdx.z, KVH = gridDim.y;
   const int rl = threadIdx.x / TPR, d = 4 * (threadIdx.x % TPR);
   const int rr = rsub * R + rl;
+  // no valid sequence has a row at or past rows_max: such a thread loads nothing (a select
+  // of the load count, not an early return, which would put a scalar round trip for
+  // rows_max ahead of the other kernel arguments' loads)
+  const bool live = tile * 16 + rr < rows_max;
   const int64_t slot0 = ((int64_t(b) * KVH + kvh) * tiles_max + tile) * num_parts;
   const float* src = ws_acc + (slot0 * 16 + rr) * D + d;
   const float* mlp = ws_ml + 2 * (slot0 * 16 + rr);
@@ -351,7 +361,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
         vl[u] = mlp[(p0 + u) * kMlStride + 1];
       }
   };
-  load(0, min(num_parts, kBatch));
+  load(0, live ? min(num_parts, kBatch) : 0);
   const int q0 = cu_q[b];
   const int qlen = cu_q[b + 1] - q0;
   const int ctx = ctx_lens[b];
@@ -365,7 +375,7 @@ __global__ __launch_bounds__(256) void mq_combine_kernel(
   // its prefix and suffix partitions the same way)
   const int nparts = kend > 0 ? (kend + P - 1) / P : 1;
   const int row = r0 + rr;
-  if (nparts <= 1 || row >= rows) return;  // nparts 1: written by the attention kernel
+  if (!live || nparts <= 1 || row >= rows) return;  // nparts 1: written by the attention kernel
   float M = -INFINITY, L = 0.f;
   f32x4 A = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int p0 = 0; p0 < nparts; p0 += kBatch) {
@@ -602,7 +612,8 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
   }
   const int num_parts = max_ctx > 0 ? (max_ctx + P - 1) / P : 1;
   DSP_HOST_CHECK(num_parts <= kMaxParts, DSP_EINVAL);
-  DSP_HOST_CHECK(tiles * num_parts < (int64_t(1) << 31), DSP_EINVAL);
+  DSP_HOST_CHECK(tiles * num_parts < (int64_t(1) << 31) && tiles * 16 < (int64_t(1) << 31),
+                 DSP_EINVAL);
   const size_t need = fixed_mq_workspace_bytes(B, Hq, KVH, D, max_q_len, max_ctx, P);
   DSP_HOST_CHECK(workspace_bytes >= need && (need == 0 || workspace != nullptr), DSP_EWORKSPACE);
   DSP_HOST_CHECK(need == 0 || dsp_aligned(workspace, 16), DSP_EALIGN);
@@ -649,14 +660,16 @@ int mq_attention_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                              oh, o_stride_t, o_stride_h, err_count);
   }
   if (st != DSP_OK || ws_parts <= 1) return st;
-  dim3 cgrid(static_cast<unsigned>(tiles * 16 / mq_combine_rows(D)), static_cast<unsigned>(KVH),
+  const int32_t rows_max = max_q_len * G;  // <= tiles * 16 < 2^31 (checked above)
+  const int R = mq_combine_rows(D);
+  dim3 cgrid(static_cast<unsigned>((rows_max + R - 1) / R), static_cast<unsigned>(KVH),
              static_cast<unsigned>(B));
   if (!f16)
     return launch_mq_combine<Bf16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
-                                      ws_parts, tm, prefix_tokens, oh, o_stride_t,
+                                      ws_parts, tm, prefix_tokens, rows_max, oh, o_stride_t,
                                       o_stride_h);
   return launch_mq_combine<F16Tag>(D, cgrid, s, ws_acc, ws_ml, cu_q, ctx_lens, max_ctx, G, P,
-                                   ws_parts, tm, prefix_tokens, oh, o_stride_t,
+                                   ws_parts, tm, prefix_tokens, rows_max, oh, o_stride_t,
                                    o_stride_h);
 }
 

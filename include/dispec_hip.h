@@ -244,8 +244,9 @@ int dsp_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride
  *   max_q_len  : upper bound of q_len_b (sizes the grid and the workspace).  A larger
  *                q_len_b is a caller error that never leads to an out-of-bounds access:
  *                the balanced split counts it in err_count and writes the sequence's first
- *                max_q_len query rows as zeros; the tiled kernels compute only the rows
- *                their max_q_len-sized grid covers.
+ *                max_q_len query rows as zeros; the tiled kernels compute its first
+ *                max_q_len query rows (rows past them are computed or left untouched,
+ *                depending on the split).
  *   partition_tokens : split-K key partition (multiple of 128, at most 64 partitions of
  *                max_ctx); 0 picks one from the shape.  More than one partition needs
  *                `workspace` (dsp_paged_mq_workspace_bytes with the same partition_tokens,
