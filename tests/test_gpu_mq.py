@@ -18,7 +18,7 @@ DEV = "cuda"
 
 
 def _run(q_lens, ctx_lens, Hq, KVH, D, seed, dtype=torch.bfloat16, tables=None, NB=None,
-         bs=16):
+         bs=16, P=0):
     from dispec_amd.engine.hip_attn import paged_mq_attention
     G = Hq // KVH
     if tables is None:
@@ -35,7 +35,7 @@ def _run(q_lens, ctx_lens, Hq, KVH, D, seed, dtype=torch.bfloat16, tables=None, 
     cu = torch.tensor([0] + list(np.cumsum(q_lens)), dtype=torch.int32)
     out = paged_mq_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), bt.to(DEV), cu.to(DEV),
                              torch.tensor(ctx_lens, dtype=torch.int32).to(DEV), G, block_size=bs,
-                             max_q_len=max(q_lens))
+                             max_q_len=max(q_lens), partition_tokens=P)
     slot_lists = [ref_cpu.context_slots(t, n, bs) for t, n in zip(tables, ctx_lens)]
     ref = ref_cpu.mq_attention(f64(q), f64(kc), f64(vc), slot_lists, q_lens, G)
     return f64(out), ref
@@ -64,6 +64,17 @@ def test_chunked_fresh_and_decode_rows_in_one_batch(dtype):
     ctx = [40, 6, 11, 33, 1]
     out, ref = _run(q_lens, ctx, 4, 2, 64, 50, dtype)
     assert_attention_close(out, ref, f"mixed batch {dtype}")
+
+
+@pytest.mark.parametrize("D", [32, 64, 128])
+@pytest.mark.parametrize("Hq,KVH", [(16, 8), (12, 2)])
+@pytest.mark.parametrize("q_lens", [[1, 1, 1], [3, 1, 2]], ids=["one-query", "three-query"])
+def test_merge_of_short_query_blocks(q_lens, Hq, KVH, D):
+    """Short query blocks over several key partitions: the merge's grid covers only the
+    packed rows below max_q_len * G (2, 6 or 18 here, of 16-row tiles), and every row of
+    every sequence still matches the oracle."""
+    out, ref = _run(q_lens, [700, 1300, 260], Hq, KVH, D, 70 + D + Hq + len(q_lens), P=128)
+    assert_attention_close(out, ref, f"q_lens={q_lens} D={D} Hq={Hq} KVH={KVH}")
 
 
 @pytest.mark.parametrize("D", [32, 64, 128])
