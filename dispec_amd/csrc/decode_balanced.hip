@@ -86,13 +86,16 @@ __device__ __forceinline__ int wave_sum(int v) {
 __device__ __forceinline__ bool mq_bad(int ql, int ctx, int max_q_len, int max_ctx) {
   return ql > max_q_len || ctx < ql || ctx > max_ctx;
 }
+__device__ __forceinline__ int units_for(bool mq, int ql, int ctx, int max_ctx, int max_q_len) {
+  if (!mq) return units_of(ctx, max_ctx);
+  return (ql <= 0 || mq_bad(ql, ctx, max_q_len, max_ctx)) ? 0 : units_of(ctx, max_ctx);
+}
 __device__ __forceinline__ int seq_units(const int32_t* __restrict__ ctx_lens,
                                          const int32_t* __restrict__ cu_q, int b, int max_ctx,
                                          int max_q_len) {
   const int ctx = ctx_lens[b];
-  if (cu_q == nullptr) return units_of(ctx, max_ctx);
-  const int ql = cu_q[b + 1] - cu_q[b];
-  return (ql <= 0 || mq_bad(ql, ctx, max_q_len, max_ctx)) ? 0 : units_of(ctx, max_ctx);
+  const int ql = cu_q ? cu_q[b + 1] - cu_q[b] : 1;
+  return units_for(cu_q != nullptr, ql, ctx, max_ctx, max_q_len);
 }
 
 // Units of one KV head summed over all sequences (the whole launch is KVH times this).
@@ -449,23 +452,35 @@ __global__ __launch_bounds__(256) void decode_balanced_combine_kernel(
   __shared__ float s_ml[4][2];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int h = blockIdx.x, b = blockIdx.y, i = blockIdx.z;
-  const int q0 = cu_q ? cu_q[b] : b;
-  const int ql = cu_q ? cu_q[b + 1] - q0 : 1;
-  if (i >= ql) return;
   const int maxq = RPH / G;  // max_q_len (the grid's z extent)
-  // total units, and the units of the sequences before b, from one scan per 64 sequences
+  // One scan per 64 sequences gives the total units and the units of the sequences before
+  // b; sequence b's own lengths are read out of the same lanes (readlane), so the merge
+  // waits on one memory round trip before its pieces: no separate loads of cu_q[b] or
+  // ctx_lens[b] ahead of the scan or behind it.
   int64_t total = 0, pre = 0;
+  int q0 = b, ql = 1, raw = 0, nb = 0;
+  const bool mq = cu_q != nullptr;
   for (int b0 = 0; b0 < B; b0 += 64) {
     const int bb = b0 + lane;
-    const int incl = wave_incl_scan(bb < B ? seq_units(ctx_lens, cu_q, bb, max_ctx, maxq) : 0);
-    if (b >= b0 && b < b0 + 64)
-      pre = total + (b > b0 ? __builtin_amdgcn_readlane(incl, b - b0 - 1) : 0);
+    const bool in = bb < B;
+    const int ctx = in ? ctx_lens[bb] : 0;
+    const int c0 = in && mq ? cu_q[bb] : bb;
+    const int c1 = in && mq ? cu_q[bb + 1] : bb + 1;
+    const int u = in ? units_for(mq, c1 - c0, ctx, max_ctx, maxq) : 0;
+    const int incl = wave_incl_scan(u);
+    if (b >= b0 && b < b0 + 64) {  // wave-uniform
+      const int l = b - b0;
+      pre = total + (l > 0 ? __builtin_amdgcn_readlane(incl, l - 1) : 0);
+      q0 = __builtin_amdgcn_readlane(c0, l);
+      ql = __builtin_amdgcn_readlane(c1, l) - q0;
+      raw = __builtin_amdgcn_readlane(ctx, l);
+      nb = __builtin_amdgcn_readlane(u, l);
+    }
     total += __builtin_amdgcn_readlane(incl, 63);
   }
-  const int raw = ctx_lens[b];
-  const bool bad = cu_q ? mq_bad(ql, raw, maxq, max_ctx) : (raw < 0 || raw > max_ctx);
+  if (i >= ql) return;
+  const bool bad = mq ? mq_bad(ql, raw, maxq, max_ctx) : (raw < 0 || raw > max_ctx);
   if (h == 0 && i == 0 && threadIdx.x == 0 && err_count && bad) atomicAdd(err_count, 1);
-  const int nb = seq_units(ctx_lens, cu_q, b, max_ctx, maxq);
   uint16_t* o = out + int64_t(q0 + i) * osb + int64_t(h) * osh;
   if (nb == 0) {
     if (threadIdx.x < D) o[threadIdx.x] = 0;
