@@ -86,6 +86,19 @@ def test_ragged_empty_and_fresh_blocks():
     assert_attention_close(out, ref, "ragged")
 
 
+def test_more_sequences_than_one_scan_block():
+    """150 sequences (the merge reads each sequence's lengths out of a 64-lane scan block:
+    here three blocks), ragged query blocks of 0-5 rows, contexts 5-700, and one long
+    context late in the batch so that its pieces are merged from the third block."""
+    g = torch.Generator().manual_seed(760)
+    q_lens = torch.randint(0, 6, (150,), generator=g).tolist()
+    ctx = [max(q, int(c)) for q, c in zip(q_lens, torch.randint(5, 701, (150,), generator=g))]
+    ctx[140] = 6000
+    q_lens[140] = 5
+    out, ref = _run(q_lens, ctx, 16, 8, 128, 761)
+    assert_attention_close(out, ref, "150 sequences")
+
+
 def test_one_long_context_among_short_ones():
     """One 12k context beside 15 of 100-600: the long one is split over many workers and
     its pieces merged; the short ones mostly run whole."""
