@@ -409,6 +409,14 @@ def bench_c2(torch) -> dict:
            "c2_append_prefill_rows": n_rows, "c2_append_prefill_us": app_s * 1e6,
            "c2_append_prefill_GBps": app_bytes / app_s / 1e9,
            "c2_append_prefill_warm_GBps": app_bytes / app_warm_s / 1e9}
+    # roofline object of the decode launch (balanced kernel + merge) against HBM: the
+    # contexts' K and V read once, plus q, out, block table and lengths; traffic from the
+    # counter passes in profiles/decode_c2_traffic.md
+    alg = kv_bytes + 2 * B * Hq * D * 2 + bt.numel() * 4 + B * 4
+    res["c2_decode_roofline"] = {
+        "bound": "hbm", "achieved": round(alg / dec_s / 1e9, 1), "peak": PEAK_HBM_GBPS,
+        "unit": "GB/s", "frac": round(alg / dec_s / 1e9 / PEAK_HBM_GBPS, 4),
+        "traffic": _traffic_per_launch("decode_c2_traffic.md"), "alg_bytes_per_launch": alg}
     del cache, kp, vp
     torch.cuda.empty_cache()
     return res
@@ -748,6 +756,15 @@ def bench_c4(torch) -> dict:
         "c4_evict_GBps": 2 * 2 * L * nev * cache.block_bytes / ev_s / 1e9,
         "c4_evict_warm_GBps": 2 * 2 * L * nev * cache.block_bytes / ev_warm_s / 1e9,
     }
+    # roofline object of the shared-prefix verify launch (attention + merge) against HBM:
+    # the unique K/V (shared prompt once, each sequence's own tokens once), q and out;
+    # traffic from the counter passes in profiles/verify_c4_traffic.md
+    alg = unique_tokens * KVH * D * 4 + 2 * S * K * Hq * D * 2
+    res["c4_verify_roofline"] = {
+        "bound": "hbm", "achieved": round(alg / ver_s / 1e9, 1), "peak": PEAK_HBM_GBPS,
+        "unit": "GB/s", "frac": round(alg / ver_s / 1e9 / PEAK_HBM_GBPS, 4),
+        "traffic": _traffic_per_launch("verify_c4_traffic.md", "c4_verify"),
+        "alg_bytes_per_launch": alg}
     del cache, spill
     torch.cuda.empty_cache()
     return res
