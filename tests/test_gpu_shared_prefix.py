@@ -70,6 +70,15 @@ def test_config4_verify_shape(hip):
     assert_attention_close(out, ref, "config 4 shared prefix")
 
 
+def test_config4_fork_decode_shape(hip):
+    """The decode step of the same 32 forks (one query each) through the shared-prefix
+    launch, as ModelRunner routes it: the merge covers 2 of each 16-row tile's rows."""
+    suffix = [2 + s + 1 for s in torch.randint(64, 513, (32,), generator=gen(502)).tolist()]
+    out, ref, err = _run([1] * 32, suffix, 128, 16, 8, 128, 503, prefix=2048)
+    assert err == 0
+    assert_attention_close(out, ref, "config 4 fork decode")
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("Hq,KVH", [(16, 8), (32, 8), (14, 2), (12, 2)])
 def test_groups_and_head_dims(hip, D, Hq, KVH):
