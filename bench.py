@@ -858,7 +858,7 @@ def _xfer_time(torch, step, iters=4) -> float:
 
 
 def bench_xfer(torch) -> dict:
-    """Escalation handoff over TCP (§8(f) 3): export (J5a gather) -> TcpTransport.send ->
+    """Escalation handoff over TCP (the raw wire format): export (J5a gather) -> TcpTransport.send ->
     loopback socket -> TcpTransport.recv into GPU memory -> import (J5c scatter), sender
     and receiver in two threads of this process.  GB/s = K + V payload bytes / wall time
     of one handoff; the reference's pickle framing is timed in the CPU-baseline leg."""
