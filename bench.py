@@ -953,10 +953,20 @@ def bench_c5(torch) -> dict:
     w_probe = torch.empty((kv, kv), dtype=torch.bfloat16, device=dev).normal_()
     fill_s = _time_gpu(torch, fill_probe, 20)
     # the vendor library on the same problem size (hipBLASLt through torch.matmul): one
-    # (8 x 4096, 1024) x (1024, 1024) bf16 product, both operands contiguous
+    # (8 x 4096, 1024) x (1024, 1024) bf16 product repeated, so its operands stay in the
+    # Infinity Cache.  `c5_map_hipblaslt_us` takes the weight as the map kernel does (stored
+    # N x K, K contiguous: the transposed view of a contiguous matrix, a plain 2-D product),
+    # `_kn_us` as a contiguous K x N matrix; `c5_map_warm_us` is the map kernel on exactly
+    # the operands of the first (x, the same N x K weight, no bias, a contiguous output),
+    # repeated the same way -- the like-for-like figure beside them (the 72-launch loop
+    # above streams a new A from HBM for every launch).
+    from dispec_amd.kv.transfer import _gemm
     x_lib = kbuf[:R * T].view(R * T, kv)
     w_lib = w_probe.contiguous()
-    lib_s = _time_gpu(torch, lambda: torch.matmul(x_lib, w_lib), 20)
+    out_lib = torch.empty((R * T, kv), dtype=torch.bfloat16, device=dev)
+    lib_s = _time_gpu(torch, lambda: torch.matmul(x_lib, w_lib.t()), 20)
+    lib_kn_s = _time_gpu(torch, lambda: torch.matmul(x_lib, w_lib), 20)
+    warm_s = _time_gpu(torch, lambda: _gemm(x_lib, [0], kv, kv, R * T, w_lib, out_lib), 20)
     # scatter into a 36-layer target pool
     tgt = PagedKVCache(Lt, NB, bs, KVH, D, device=dev)
     perm = torch.randperm(NB, generator=gcpu)[:nb].view(R, T // bs)
@@ -1004,6 +1014,8 @@ def bench_c5(torch) -> dict:
     res["c5_map_fill_floor_us"] = round(fill_s * 1e6, 2)
     res["c5_map_us_per_launch"] = round(per_launch * 1e6, 2)
     res["c5_map_hipblaslt_us"] = round(lib_s * 1e6, 2)
+    res["c5_map_hipblaslt_kn_us"] = round(lib_kn_s * 1e6, 2)
+    res["c5_map_warm_us"] = round(warm_s * 1e6, 2)
     res["c5_map_roofline"] = {
         "bound": "mfma", "achieved": round(flops / m_s / 1e12, 1), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(flops / m_s / 1e12 / PEAK_BF16_TFLOPS, 4),
