@@ -398,7 +398,9 @@ __global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
   // n = wn + 16j + 4*(lane/16) + e of row m = wm + 16i + lane%16, so stores straight from
   // it write 16 rows x 32 bytes per instruction.  Instead each wave rounds its 64 x 128
   // outputs into its own 16 KiB of the (now idle) stage buffers as bf16 rows of 256 bytes
-  // (16-byte chunk c of row r at slot c ^ (r & 15): conflict-free both ways) and reads them
+  // (16-byte chunk c of row r at slot c ^ (r & 15), its two 8-byte halves swapped in rows
+  // with r & 8: the 16 lanes of an 8-byte write, rows r0 .. r0 + 15 at one column, then hit
+  // 16 distinct bank pairs, where rows r and r + 8 shared one) and reads them
   // back four whole rows per instruction, so C is written in full 256-byte row runs with
   // 16-byte lanes -- half the store instructions, every cache line written whole -- with
   // non-temporal stores (same-box A/B, config 5: 73.4-74.7 against 75.7-76.8 us a launch).
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
         yb[e] = dsp_f32_to_bf16(epi_bias_act(acc[i][j][e], b4[j][e], kBias, kAct));
       const int col = 16 * j + 4 * fq;
       *reinterpret_cast<dsp_u32x2*>(ct + r * (big::kTN * 2) + (((col >> 3) ^ (r & 15)) * 16) +
-                                    (col & 7) * 2) =
+                                    (((col & 7) * 2) ^ (r & 8))) =
           dsp_u32x2{uint32_t(yb[0]) | (uint32_t(yb[1]) << 16),
                     uint32_t(yb[2]) | (uint32_t(yb[3]) << 16)};
     }
@@ -449,13 +451,18 @@ __global__ __launch_bounds__(big::kNT) void map_gemm_big_kernel(
 #pragma unroll
   for (int q = 0; q < big::kTM / 4; ++q) {
     const int r = 4 * q + (lane >> 4);
-    dsp_u32x4 v =
-        *reinterpret_cast<const dsp_u32x4*>(ct + r * (big::kTN * 2) + ((cl ^ (r & 15)) * 16));
+    // r & 8 is bit 1 of q for every lane (r = 4q + 0..3): a fixed register swap
+    const bool swapped = (q >> 1) & 1;
+    auto unswap = [swapped](dsp_u32x4 u) {
+      return swapped ? dsp_u32x4{u[2], u[3], u[0], u[1]} : u;
+    };
+    dsp_u32x4 v = unswap(
+        *reinterpret_cast<const dsp_u32x4*>(ct + r * (big::kTN * 2) + ((cl ^ (r & 15)) * 16)));
     const int64_t m = m0 + wm + r;
     if (m >= M) continue;
     if constexpr (kRope) {
-      const dsp_u32x4 vp =
-          *reinterpret_cast<const dsp_u32x4*>(ct + r * (big::kTN * 2) + ((pcl ^ (r & 15)) * 16));
+      const dsp_u32x4 vp = unswap(
+          *reinterpret_cast<const dsp_u32x4*>(ct + r * (big::kTN * 2) + ((pcl ^ (r & 15)) * 16)));
       const float* cr = po.rope_cos + m * hd + d0;
       const float* sr = po.rope_sin + m * hd + d0;
       const f32x4 c0 = *reinterpret_cast<const f32x4*>(cr), c1 = *reinterpret_cast<const f32x4*>(cr + 4);
