@@ -1,4 +1,5 @@
-"""The map GEMM's two kernels against each other on seeded random problems (GPU).
+"""The map GEMM's kernels on seeded random problems (GPU): the two GEMM kernels against
+each other, and the fused map-into-pool launch against the unfused chain.
 
 `dsp_kv_map_gemm` runs problems of at least 128 output tiles of 256 x 256 on the
 direct-to-LDS kernel (256 x 256 tiles, its C tile staged through LDS with swizzled 256-byte
@@ -65,3 +66,64 @@ def test_large_and_small_tile_kernels_agree_bitwise(seed):
             f"problem {z} of M={M} N={N} B={B} layers={layers} seg={seg} bias={bias_mode} " \
             f"act={act} accum={accum}"
     assert torch.isfinite(out.float()).all()
+
+
+def _pool_case(seed):
+    rng = random.Random(seed)
+    D = rng.choice((64, 128))
+    H = rng.choice((2, 4, 8))
+    layers = tuple(rng.sample(range(3), rng.randint(1, 2)))
+    return (rng.randint(1, 4), rng.randint(40, 1500), D, H, layers, rng.random() < 0.7,
+            rng.choice((16, 32)), rng.random() < 0.3)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_fused_map_into_pool_equals_gemm_rope_scatter(seed):
+    """dsp_kv_map_gemm_to_pool (the large-tile kernel with the target RoPE and the pool
+    scatter in its epilogue, whatever the problem size) against dsp_kv_map_gemm ->
+    dsp_kv_rope -> dsp_kv_scatter on seeded random shapes: 1-4 requests of 40-1500 tokens
+    (ragged against the 256-row tiles and the blocks), 2-8 heads of 64 or 128 dims, design
+    rows of one or two source layers, RoPE on or off, 16- or 32-token blocks, sometimes a
+    block id outside the pool (skipped and counted).  Every pool byte must match."""
+    from dispec_amd import _lib
+    from dispec_amd.kv.transfer import LayerMap, _rope
+    from oracle import ref_cpu
+    from tests.test_gpu_map import _pool_pair
+    R, T, D, H, layers, rope, bs, bad_block = _pool_case(seed)
+    Ls, kv = 3, H * D
+    g = torch.Generator().manual_seed(7000 + seed)
+    src = torch.randn((R, Ls, T, kv), generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn((len(layers) * kv, kv), generator=g) / (2 * kv ** 0.5)).to(torch.bfloat16)
+    b = torch.randn(kv, generator=g).to(torch.bfloat16)
+    m = LayerMap(layers, b, weight=w).to(DEV, torch.bfloat16)
+    cos, sin = (torch.from_numpy(a).to(DEV) for a in ref_cpu.rope_tables(np.arange(T), D, 1e6))
+    per_req = -(-T // bs)
+    NB = R * per_req + 7
+    ref_c, got_c = _pool_pair(2, NB, bs, H, D, 100 + seed)
+    perm = torch.randperm(NB, generator=g)[:R * per_req].view(R, -1).to(torch.int32)
+    if bad_block:
+        perm[R - 1, per_req // 2] = NB + 1
+    table = perm.to(DEV)
+    offs = [lay * T * kv for lay in layers]
+    dense = torch.empty((R, T, kv), dtype=torch.bfloat16, device=DEV)
+    m.apply_into(src, offs, kv, kv, T, dense, batch=R, a_batch_stride=Ls * T * kv,
+                 c_batch_stride=T * kv)
+    if rope:
+        for r in range(R):
+            _rope(dense[r].view(1, T, H, D), cos, sin, +1, out=dense[r].view(1, T, H, D))
+    err_ref = torch.zeros(1, dtype=torch.int32, device=DEV)
+    cu = torch.arange(0, (R + 1) * T, T, dtype=torch.int64, device=DEV)
+    layer = ref_c.key[1]
+    _lib.check(_lib.lib().dsp_kv_scatter(
+        layer.data_ptr(), layer.data_ptr(), 1, ref_c.layer_bytes, ref_c.num_blocks,
+        ref_c.row_bytes, bs, table.data_ptr(), table.stride(0), cu.data_ptr(), R, T,
+        dense.data_ptr(), dense.data_ptr(), err_ref.data_ptr(), _lib.stream_of(dense)), "scatter")
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    assert m.apply_to_pool(src, offs, kv, kv, T, got_c.key[1], table, bs,
+                           (cos, sin) if rope else None, batch=R,
+                           a_batch_stride=Ls * T * kv, err=err)
+    torch.cuda.synchronize()
+    case = f"R={R} T={T} D={D} H={H} layers={layers} rope={rope} bs={bs} bad={bad_block}"
+    assert torch.equal(got_c.key.view(torch.int16), ref_c.key.view(torch.int16)), case
+    assert torch.equal(got_c.value.view(torch.int16), ref_c.value.view(torch.int16)), case
+    assert (int(err.item()) > 0) == bad_block and (int(err_ref.item()) > 0) == bad_block, case
