@@ -42,6 +42,8 @@ SIGNATURES: dict[str, tuple] = {
                               _P, c_int32, c_int64, _P, _P, _P, _P]),
     "dsp_kv_scatter": (c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int32, _P, c_int64,
                                _P, c_int32, c_int64, _P, _P, _P, _P]),
+    "dsp_kv_scatter_ordered": (c_int, [_P, _P, c_int64, c_int64, c_int64, c_int64, c_int32, _P,
+                                       c_int64, _P, c_int32, c_int64, _P, _P, _P, _P, _P]),
     "dsp_paged_decode_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32,
                                                       c_int32]),
     "dsp_paged_decode_partition_tokens": (c_int, [c_int32, c_int32, c_int32, c_int32]),

@@ -11,7 +11,7 @@ working.  What changes is who moves the bytes:
                                               index_copy_ launches)
   gather             -> dsp_kv_gather_slots  (:70-72)
   export_contiguous  -> dsp_kv_gather        (block-table gather over all layers, :87-90)
-  import_contiguous  -> dsp_kv_scatter       (:92-96)
+  import_contiguous  -> dsp_kv_scatter_ordered (:92-96)
   copy_blocks        -> dsp_kv_copy_blocks   (new: the data move behind copy-on-write
                                               fork and prefix-cache spill)
 
@@ -257,12 +257,20 @@ class PagedKVCache:
         k, v = k.contiguous(), v.contiguous()
         table = self.block_table(tables)
         cu_t = torch.tensor(cu, dtype=torch.long).to(self.key.device)
-        _lib.check(_lib.lib().dsp_kv_scatter(
+        self._scatter(table, cu_t, max(b - a for a, b in zip(cu[:-1], cu[1:])), k, v)
+        self._after()
+
+    def _scatter(self, table: torch.Tensor, cu_t: torch.Tensor, max_seqlen: int,
+                 k: torch.Tensor, v: torch.Tensor) -> None:
+        """dsp_kv_scatter_ordered: the copies in destination-block order when the tables
+        name at least half the pool's blocks (the library decides), with a block-owner
+        workspace from torch's stream-ordered allocator."""
+        owner = torch.empty(self.num_blocks, dtype=torch.int32, device=self.key.device)
+        _lib.check(_lib.lib().dsp_kv_scatter_ordered(
             self.key.data_ptr(), self.value.data_ptr(), self.num_layers, self.layer_bytes,
             self.num_blocks, self.row_bytes, self.block_size, table.data_ptr(), table.stride(0),
-            cu_t.data_ptr(), len(tables), max(b - a for a, b in zip(cu[:-1], cu[1:])),
-            k.data_ptr(), v.data_ptr(), self._err.data_ptr(), self._stream()), "dsp_kv_scatter")
-        self._after()
+            cu_t.data_ptr(), table.shape[0], int(max_seqlen), k.data_ptr(), v.data_ptr(),
+            owner.data_ptr(), self._err.data_ptr(), self._stream()), "dsp_kv_scatter_ordered")
 
     def import_contiguous(self, block_ids: list[int], k: torch.Tensor, v: torch.Tensor) -> None:
         """Scatter contiguous (num_layers, T, H, D) K/V into the sequence's blocks."""
@@ -303,12 +311,7 @@ class PagedKVCache:
     def scatter_from(self, block_table: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
                      k_buf: torch.Tensor, v_buf: torch.Tensor) -> None:
         """import_batch with device-side tables (the inverse of gather_into)."""
-        _lib.check(_lib.lib().dsp_kv_scatter(
-            self.key.data_ptr(), self.value.data_ptr(), self.num_layers, self.layer_bytes,
-            self.num_blocks, self.row_bytes, self.block_size, block_table.data_ptr(),
-            block_table.stride(0), cu_seqlens.data_ptr(), block_table.shape[0], int(max_seqlen),
-            k_buf.data_ptr(), v_buf.data_ptr(), self._err.data_ptr(), self._stream()),
-            "dsp_kv_scatter")
+        self._scatter(block_table, cu_seqlens, max_seqlen, k_buf, v_buf)
 
     def copy_blocks_device(self, src: "PagedKVCache", src_ids: torch.Tensor,
                            dst_ids: torch.Tensor) -> None:

@@ -154,6 +154,27 @@ int dsp_kv_scatter(void* k_pool, void* v_pool, int64_t num_layers,
                    const void* k_buf, const void* v_buf, int32_t* err_count,
                    dsp_stream_t stream);
 
+/* dsp_kv_scatter with its copies visited in destination-block order: the same rows land
+ * in the same slots (PagedKVCache.import_contiguous, paged_cache.py:92-96, batched), but
+ * the pool is written through each layer in address order and the transport buffer is
+ * read in block-sized runs out of order, which moves the bytes faster when the tables
+ * name many of the pool's blocks.  With fewer than num_blocks / 2 table entries
+ * (num_seqs * ceil(max_seqlen / block_size)) it runs dsp_kv_scatter itself.
+ *   block_owner : device int32 [num_blocks] workspace, overwritten (which table entry
+ *                 names each block); calls that overlap on one workspace race.
+ * A block named by more than one table entry (an import into sequences' own blocks never
+ * does this) is written from the last of them alone, in sequence order then block order:
+ * its rows past a partial last entry keep what the pool held.  dsp_kv_scatter writes
+ * every entry, in no defined order.  Other arguments and errors as for dsp_kv_scatter
+ * (an out-of-range block id is counted once per table entry). */
+int dsp_kv_scatter_ordered(void* k_pool, void* v_pool, int64_t num_layers,
+                           int64_t pool_layer_stride_bytes, int64_t num_blocks,
+                           int64_t row_bytes, int32_t block_size,
+                           const int32_t* block_tables, int64_t bt_stride,
+                           const int64_t* cu_seqlens, int32_t num_seqs, int64_t max_seqlen,
+                           const void* k_buf, const void* v_buf, int32_t* block_owner,
+                           int32_t* err_count, dsp_stream_t stream);
+
 /* ------------------------------------------------------------------------------ J3
  * Paged decode attention, one query token per sequence, GQA-packed and split-K.
  * Replaces batched_paged_decode_attention (dispec/engine/triton_attn.py:98-116,
