@@ -1010,6 +1010,14 @@ def bench_c5(torch) -> dict:
         "bound": "hbm", "achieved": round(moved / g_s / 1e9, 1), "peak": PEAK_HBM_GBPS,
         "unit": "GB/s", "frac": round(moved / g_s / 1e9 / PEAK_HBM_GBPS, 4),
         "traffic": _traffic_per_launch(movers, "c5_gather"), "alg_bytes_per_launch": moved}
+    # the import scatter (destination-block order): every target row read once from the
+    # transport buffers and written once into the pool; the owner fill and lookup launches
+    # before it are inside the timed call
+    scattered = 2 * 2 * Lt * R * T * tgt.row_bytes
+    res["c5_scatter_roofline"] = {
+        "bound": "hbm", "achieved": round(scattered / s_s / 1e9, 1), "peak": PEAK_HBM_GBPS,
+        "unit": "GB/s", "frac": round(scattered / s_s / 1e9 / PEAK_HBM_GBPS, 4),
+        "traffic": _traffic_per_launch(movers, "c5_scatter"), "alg_bytes_per_launch": scattered}
     per_launch = m_s / (2 * len(maps))
     res["c5_map_fill_floor_us"] = round(fill_s * 1e6, 2)
     res["c5_map_us_per_launch"] = round(per_launch * 1e6, 2)

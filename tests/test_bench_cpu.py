@@ -34,6 +34,7 @@ def test_no_gpu_exits_with_a_message():
     ("decode_c2_traffic.md", ""),                       # c2_decode_roofline
     ("verify_c4_traffic.md", "c4_verify"),              # c4_verify_roofline
     ("byte_movers_c4_c5_traffic.md", "c5_gather"),      # c5_gather_roofline
+    ("byte_movers_c4_c5_traffic.md", "c5_scatter"),     # c5_scatter_roofline
     ("byte_movers_c4_c5_traffic.md", "c5_map"),         # c5_map_roofline
 ])
 def test_every_roofline_finds_its_counter_traffic(profile, key):
